@@ -1,0 +1,358 @@
+"""Benchmark of the kernels-community-rs hot paths on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline OP] [--only OP,...]
+
+A "step" is one call of an op over its BASELINE.json configuration with inputs
+already resident in HBM. The headline op (default: FA2 forward, causal, B=4
+Hq=32 Hkv=8 S=4096 D=128 bf16) gives `value`; every op
+measured is listed under "ops" with its own throughput and roofline fraction.
+Timing: HIP events recorded on the stream the kernels are launched on (torch's
+current stream, which the ops pass to the C ABI), around exactly K steps
+bracketed by torch.cuda.synchronize().
+
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "kernels-community-rs_amd"))
+
+import torch  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, GB/s
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+
+METRIC = "FA2 fwd/bwd TFLOP/s (% bf16 MFMA peak) at S=4k D=128; RMSNorm/act HBM GB/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------
+# Workloads. Each returns (run, work, unit, bound, sample_fn).
+# --------------------------------------------------------------------------
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def wl_rmsnorm():
+    import rmsnorm
+
+    g = _gen(1)
+    rows, n = 16384, 4096
+    x = torch.randn(rows, n, generator=g).bfloat16().cuda()
+    w = (torch.rand(n, generator=g) + 0.5).bfloat16().cuda()
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, device="cuda")
+
+    def run():
+        rmsnorm.ops.rms_norm_forward(y, rstd, x, w, 1e-6, 0.0, "llama")
+
+    bytes_ = rows * n * 2 * 2 + n * 2 + rows * 4  # read x, w; write y, rstd
+    return dict(run=run, work=bytes_, bound="hbm", kernel="rms_fwd_wave",
+                config={"x": [rows, n], "dtype": "bf16", "eps": 1e-6, "casting_mode": "llama"},
+                cpu=lambda: cpu_rmsnorm(x, w))
+
+
+def _wl_gated(op):
+    def make():
+        import activation_rs
+
+        g = _gen(2)
+        tokens, d2 = 16384, 28672
+        x = torch.randn(tokens, d2, generator=g).bfloat16().cuda()
+        out = torch.empty(tokens, d2 // 2, dtype=x.dtype, device="cuda")
+        fn = getattr(activation_rs.ops, op)
+
+        def run():
+            fn(out, x)
+
+        bytes_ = tokens * d2 * 2 + tokens * (d2 // 2) * 2
+        return dict(run=run, work=bytes_, bound="hbm", kernel="act_and_mul_vec",
+                    config={"x": [tokens, d2], "out": [tokens, d2 // 2], "dtype": "bf16"},
+                    cpu=lambda: cpu_gated(op, x))
+
+    return make
+
+
+def _attn_inputs(seed, b=4, hq=32, hkv=8, s=4096, d=128):
+    g = _gen(seed)
+    q = torch.randn(b, s, hq, d, generator=g).bfloat16().cuda()
+    k = torch.randn(b, s, hkv, d, generator=g).bfloat16().cuda()
+    v = torch.randn(b, s, hkv, d, generator=g).bfloat16().cuda()
+    return q, k, v
+
+
+def _wl_fa_fwd(causal):
+    def make():
+        import flash_attn2_rs
+
+        b, hq, hkv, s, d = 4, 32, 8, 4096, 128
+        q, k, v = _attn_inputs(3, b, hq, hkv, s, d)
+        out = torch.empty_like(q)
+        ops = flash_attn2_rs.ops
+
+        def run():
+            ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, out)
+
+        flops = 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
+        return dict(run=run, work=flops, bound="mfma", kernel="flash_fwd",
+                    config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
+                            "dtype": "bf16"},
+                    cpu=lambda: cpu_attention(q, k, v, causal))
+
+    return make
+
+
+def _wl_fa_bwd(causal):
+    def make():
+        import flash_attn2_rs
+
+        b, hq, hkv, s, d = 4, 32, 8, 4096, 128
+        q, k, v = _attn_inputs(3, b, hq, hkv, s, d)
+        g = _gen(4)
+        dout = torch.randn(b, s, hq, d, generator=g).bfloat16().cuda()
+        out = torch.empty_like(q)
+        ops = flash_attn2_rs.ops
+        lse = ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, out)
+        args = (None, None, causal, -1, -1, 0.0, 0.0, None)
+
+        def run():
+            delta = ops.bwd_preprocess(dout, out, 0.0)
+            ops.bwd_all(q, k, v, dout, lse, delta, *args)
+
+        flops = 2.5 * 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
+        return dict(run=run, work=flops, bound="mfma", kernel="flash_bwd",
+                    config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
+                            "dtype": "bf16"},
+                    cpu=None)
+
+    return make
+
+
+def varlen_lengths(seed=5, count=16, lo=128, hi=8192):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (count,), generator=g).tolist()
+
+
+def _wl_fa_varlen(kind):
+    def make():
+        import flash_attn2_rs
+
+        lens = varlen_lengths()
+        hq, hkv, d = 32, 8, 128
+        total = sum(lens)
+        cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32).cuda()
+        g = _gen(6)
+        q = torch.randn(total, hq, d, generator=g).bfloat16().cuda()
+        k = torch.randn(total, hkv, d, generator=g).bfloat16().cuda()
+        v = torch.randn(total, hkv, d, generator=g).bfloat16().cuda()
+        ops = flash_attn2_rs.ops
+        mx = max(lens)
+        fwd_args = (q, k, v, cu, cu, None, None, None, None, True, -1, -1, 0.0, 0.0, None, mx, mx,
+                    False, False)
+        sum_sq = sum(l * l for l in lens)
+        fwd_flops = 4.0 * hq * d * sum_sq * 0.5
+        if kind == "fwd":
+            def run():
+                ops.varlen_fwd_explicit(*fwd_args)
+
+            work = fwd_flops
+        else:
+            out, lse, _ = ops.varlen_fwd_explicit(*fwd_args)
+            dout = torch.randn(total, hq, d, generator=g).bfloat16().cuda()
+
+            def run():
+                ops.varlen_bwd_explicit(q, k, v, dout, out, lse, cu, cu, None, None, True, -1, -1,
+                                        0.0, 0.0, None, mx, mx, False)
+
+            work = 2.5 * fwd_flops
+        return dict(run=run, work=work, bound="mfma", kernel=f"flash_varlen_{kind}",
+                    config={"seqs": len(lens), "sum_L": total, "sum_L2": sum_sq, "Hq": hq,
+                            "Hkv": hkv, "D": d, "causal": True, "dtype": "bf16"},
+                    cpu=None)
+
+    return make
+
+
+WORKLOADS = {
+    "fa_fwd_causal": _wl_fa_fwd(True),
+    "fa_fwd": _wl_fa_fwd(False),
+    "fa_bwd_causal": _wl_fa_bwd(True),
+    "fa_bwd": _wl_fa_bwd(False),
+    "fa_varlen_fwd": _wl_fa_varlen("fwd"),
+    "fa_varlen_bwd": _wl_fa_varlen("bwd"),
+    "rms_norm": wl_rmsnorm,
+    "silu_and_mul": _wl_gated("silu_and_mul"),
+    "gelu_and_mul": _wl_gated("gelu_and_mul"),
+    "gelu_tanh_and_mul": _wl_gated("gelu_tanh_and_mul"),
+}
+
+# --------------------------------------------------------------------------
+# CPU baselines: the oracle (the tests' formulas restated in numpy), timed on a
+# bounded sample on this host, scaled to the metric's unit.
+# --------------------------------------------------------------------------
+
+
+def _timed(fn, min_runs=3, budget_s=8.0):
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < 7):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_gated(op, x):
+    from oracle import activation as A
+
+    rows = 256
+    sample = x[:rows].float().cpu().numpy()
+    t = _timed(lambda: A.gated(op, sample, "bf16"))
+    bytes_ = rows * x.shape[1] * 2 * 1.5
+    return {"value": bytes_ / t / 1e9, "unit": "GB/s", "sample": f"oracle.activation.gated on {rows} of {x.shape[0]} rows"}
+
+
+def cpu_rmsnorm(x, w):
+    from oracle import rmsnorm as R
+
+    rows = 1024
+    sample = x[:rows].float().cpu().numpy()
+    wn = w.float().cpu().numpy()
+    t = _timed(lambda: R.forward(sample, wn, 1e-6, 0.0, "llama", "bf16"))
+    bytes_ = rows * x.shape[1] * 2 * 2
+    return {"value": bytes_ / t / 1e9, "unit": "GB/s", "sample": f"oracle.rmsnorm.forward on {rows} of {x.shape[0]} rows"}
+
+
+def cpu_attention(q, k, v, causal):
+    from oracle import attention as OA
+
+    # One (batch, kv-group) slice: 4 query heads sharing one KV head, all 4096 rows.
+    qs = q[:1, :, :4].float().cpu().numpy()
+    ks = k[:1, :, :1].float().cpu().numpy()
+    vs = v[:1, :, :1].float().cpu().numpy()
+    t = _timed(lambda: OA.forward(qs, ks, vs, causal=causal), min_runs=2, budget_s=15.0)
+    s, d = q.shape[1], q.shape[3]
+    flops = 4.0 * 4 * s * s * d * (0.5 if causal else 1.0)
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s",
+            "sample": "oracle.attention.forward (numpy f32) on batch 0, query heads 0-3 / KV head 0, S=4096"}
+
+
+# --------------------------------------------------------------------------
+
+
+def measure(name, steps, warmup):
+    wl = WORKLOADS[name]()
+    run = wl["run"]
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    if wl["bound"] == "hbm":
+        achieved = wl["work"] / (ms * 1e-3) / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    else:
+        achieved = wl["work"] / (ms * 1e-3) / 1e12
+        peak, unit = PEAK_BF16_TFLOPS, "TFLOP/s"
+    return wl, ms, achieved, peak, unit
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--headline", default="fa_fwd_causal")
+    ap.add_argument("--only", default=None, help="comma-separated workloads (default: all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (every box in this run has one); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py is single-GPU; launch it without torch.distributed.run", file=sys.stderr)
+        sys.exit(2)
+
+    names = args.only.split(",") if args.only else list(WORKLOADS)
+    if args.headline not in names:
+        names.insert(0, args.headline)
+    results = {}
+    headline = None
+    for name in names:
+        log(f"[bench] {name} ...")
+        try:
+            wl, ms, achieved, peak, unit = measure(name, args.steps, args.warmup)
+        except Exception as e:  # an op that is not built yet is reported, not fatal
+            log(f"[bench] {name} failed: {type(e).__name__}: {e}")
+            results[name] = {"error": f"{type(e).__name__}: {e}"}
+            continue
+        results[name] = {"value": round(achieved, 2), "unit": unit, "ms": round(ms, 4),
+                         "frac_of_peak": round(achieved / peak, 4), "config": wl["config"]}
+        log(f"[bench] {name}: {ms:.4f} ms, {achieved:.1f} {unit} ({achieved / peak:.1%} of peak)")
+        if name == args.headline:
+            headline = (wl, ms, achieved, peak, unit)
+
+    if headline is None:
+        print(json.dumps({"metric": METRIC, "value": None, "error": results.get(args.headline)}))
+        sys.exit(1)
+    wl, ms, achieved, peak, unit = headline
+    cpu = None
+    if not args.no_cpu and wl.get("cpu") is not None:
+        log("[bench] cpu baseline ...")
+        torch.set_num_threads(os.cpu_count() or 1)
+        cpu = wl["cpu"]()
+        cpu["cores"] = torch.get_num_threads()
+        cpu["kind"] = "port"
+        cpu["cpu"] = platform.processor() or platform.machine()
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(wl["kernel"])
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 2),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.randn, BASELINE.json shapes)",
+        "config": {"workload": args.headline, **wl["config"]},
+        "roofline": {"bound": wl["bound"], "achieved": round(achieved, 2), "peak": peak,
+                     "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "ops": results,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

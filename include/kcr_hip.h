@@ -1,0 +1,187 @@
+/*
+ * kcr_hip.h -- C ABI of libkcr_hip.so, the MI355X (gfx950) implementation of the
+ * kernels-community-rs hot paths: FlashAttention-2 (dense, varlen, backward),
+ * RMSNorm and the gated / element-wise activations.
+ *
+ * Every entry point replaces one tvm-ffi export of the reference. The reference
+ * exports take tvm-ffi `Tensor` handles (DLPack tensors); this ABI takes the same
+ * information as a plain `kcr_tensor` (data pointer, dtype, shape, element strides,
+ * device ordinal). Outputs that the reference allocates through
+ * `TVMFFIEnvTensorAlloc` (host/mod.rs:42-74 in flash-attn2-rs) are passed in
+ * preallocated by the caller instead; the caller's allocator is the one the
+ * reference would have used.
+ *
+ * Conventions
+ *   - Return value: KCR_OK (0) or one of the error kinds below; the message is
+ *     available from kcr_last_error() on the calling thread. The kinds mirror the
+ *     tvm-ffi error kinds the reference raises (ValueError / TypeError /
+ *     RuntimeError), and the messages carry the same substrings the reference
+ *     tests match ("out must have shape", "must be even", "same dtype", ...).
+ *   - `stream` is a hipStream_t. Every launch is asynchronous on that stream;
+ *     no entry point synchronises the host.
+ *   - Optional tensors are passed as NULL.
+ *   - Tensors must live on the current HIP device.
+ */
+#ifndef KCR_HIP_H
+#define KCR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum kcr_dtype {
+    KCR_FLOAT32 = 0,
+    KCR_FLOAT16 = 1,
+    KCR_BFLOAT16 = 2,
+    KCR_INT32 = 3,
+    KCR_INT64 = 4,
+    KCR_FLOAT64 = 5,
+    KCR_DTYPE_OTHER = 99
+};
+
+enum kcr_status {
+    KCR_OK = 0,
+    KCR_VALUE_ERROR = 1,
+    KCR_TYPE_ERROR = 2,
+    KCR_RUNTIME_ERROR = 3
+};
+
+#define KCR_MAX_DIMS 8
+
+/* A strided device tensor: the DLPack fields the reference reads from a tvm-ffi Tensor. */
+typedef struct kcr_tensor {
+    void* data;                      /* address of element [0, ..., 0] */
+    int32_t dtype;                   /* enum kcr_dtype */
+    int32_t ndim;                    /* 0 .. KCR_MAX_DIMS */
+    int32_t device;                  /* HIP device ordinal */
+    int32_t reserved;                /* must be 0 */
+    int64_t shape[KCR_MAX_DIMS];
+    int64_t strides[KCR_MAX_DIMS];   /* in elements */
+} kcr_tensor;
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* kcr_last_error(void);
+/* Library version string. */
+const char* kcr_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* activation-rs: activation-rs/src/ops.rs:196-265                           */
+/* ------------------------------------------------------------------------ */
+/* out[..., d] = act(input[..., :d]) * input[..., d:]  (ops.rs:200-217)      */
+/* replaces tvm export `silu_and_mul` (activation-rs/src/ops.rs:200, 255)    */
+int kcr_silu_and_mul(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+/* replaces `mul_and_silu` (ops.rs:204-207, 256): input[..., :d] * silu(input[..., d:]) */
+int kcr_mul_and_silu(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+/* replaces `gelu_and_mul` (ops.rs:209-212, 257): exact erf GELU */
+int kcr_gelu_and_mul(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+/* replaces `gelu_tanh_and_mul` (ops.rs:214-217, 258) */
+int kcr_gelu_tanh_and_mul(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+/* replaces `fatrelu_and_mul` (ops.rs:219-223, 259) */
+int kcr_fatrelu_and_mul(const kcr_tensor* out, const kcr_tensor* input, double threshold,
+                        void* stream);
+/* element-wise: out = act(input). Replace `gelu`, `gelu_tanh`, `gelu_new`,
+ * `gelu_fast`, `gelu_quick`, `silu` (ops.rs:225-253, 260-265) */
+int kcr_gelu(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+int kcr_gelu_tanh(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+int kcr_gelu_new(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+int kcr_gelu_fast(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+int kcr_gelu_quick(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+int kcr_silu(const kcr_tensor* out, const kcr_tensor* input, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* rmsnorm: rmsnorm/src/ops.rs:237-444                                       */
+/* ------------------------------------------------------------------------ */
+/* casting_mode: "llama", "gemma" or "none" (rmsnorm/src/ops.rs:28-37).      */
+/* replaces `rms_norm_forward(y, rstd, x, weight, eps, offset, casting_mode)` */
+/* (rmsnorm/src/ops.rs:237-265, 442)                                          */
+int kcr_rms_norm_forward(const kcr_tensor* y, const kcr_tensor* rstd, const kcr_tensor* x,
+                         const kcr_tensor* weight /* nullable */, double eps, double offset,
+                         const char* casting_mode, void* stream);
+/* replaces `rms_norm_backward(dx, dw_partial, dy, x, weight, rstd, offset, casting_mode)` */
+/* (rmsnorm/src/ops.rs:326-380, 443). dy == NULL: the gradient is read from dx   */
+/* and overwritten (in place).                                                   */
+int kcr_rms_norm_backward(const kcr_tensor* dx, const kcr_tensor* dw_partial /* nullable */,
+                          const kcr_tensor* dy /* nullable */, const kcr_tensor* x,
+                          const kcr_tensor* weight /* nullable */, const kcr_tensor* rstd,
+                          double offset, const char* casting_mode, void* stream);
+/* replaces `rms_norm_reduce_weight_grad(dw, dw_partial)` (rmsnorm/src/ops.rs:383-440, 444) */
+int kcr_rms_norm_reduce_weight_grad(const kcr_tensor* dw, const kcr_tensor* dw_partial,
+                                    void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* flash-attn2-rs                                                           */
+/* ------------------------------------------------------------------------ */
+/* Scalars common to the attention entry points:
+ *   has_scale/scale : softmax scale; has_scale == 0 means None (D^-0.5)
+ *   causal          : bottom-right aligned causal mask (col > row + Sk - Sq masked)
+ *   window_left/right: sliding window, -1 = unbounded (host/forward/mod.rs:310-328)
+ *   softcap         : 0 = off; else scores = softcap * tanh(qk * scale / softcap)
+ *   alibi           : float32 [H] or [B, H] slopes, nullable
+ */
+
+/* Dense forward. replaces `fwd_lse(q,k,v,alibi,scale,causal,wl,wr,softcap,out)`
+ * (flash-attn2-rs/src/host/forward/mod.rs:835-853; arities mod.rs:53-61) and the
+ * p_dropout == 0 form of `fwd` (mod.rs:815-833).
+ *   q [B,Sq,H,D], k/v [B,Sk,Hk,D] fp16/bf16, last stride 1;
+ *   out like q (written), lse float32 contiguous [B,H,Sq] (written). */
+int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                  const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                  int64_t window_left, int64_t window_right, double softcap,
+                  const kcr_tensor* out, const kcr_tensor* lse, void* stream);
+
+/* Varlen forward. replaces the plain (non-paged, non-cached, p == 0) form of
+ * `varlen_fwd_explicit(q,k,v,cuq,cuk,seqused_k,leftpad_k,alibi,scale,causal,
+ * left,right,softcap,p,state,max_q,max_k,return_softmax,zero_tensors)`
+ * (flash-attn2-rs/src/host/varlen/mod.rs:21-670).
+ *   q [Tq,H,D], k/v [Tk,Hk,D]; cu_seqlens_q/k int32 [B+1]; seqused_k, leftpad_k
+ *   int32 [B] nullable; out like q; lse float32 contiguous [H, Tq]. */
+int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                         const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
+                         const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
+                         const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                         int64_t window_left, int64_t window_right, double softcap,
+                         int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
+                         const kcr_tensor* out, const kcr_tensor* lse, void* stream);
+
+/* Backward preprocess. replaces `bwd_preprocess(dout, out, p)`
+ * (flash-attn2-rs/src/host/backward.rs:628-737):
+ *   delta[b,h,s] = sum_d dout*out * (1-p), float32 [B,H,round128(Sq)], rows >= Sq are 0. */
+int kcr_flash_bwd_preprocess(const kcr_tensor* dout, const kcr_tensor* out, double p_dropout,
+                             const kcr_tensor* delta, void* stream);
+
+/* Dense backward. replaces `bwd_dq`, `bwd_dkv` and `bwd_all`
+ * (flash-attn2-rs/src/host/backward.rs:14-626) with p_dropout == 0.
+ *   dq like q, dk/dv like k (GQA-summed, contiguous [B,Sk,Hk,D]); any of dq, dk/dv
+ *   may be NULL to skip that component (bwd_dq: dk = dv = NULL; bwd_dkv: dq = NULL).
+ *   workspace: float32 scratch, see kcr_flash_bwd_workspace_bytes(). */
+int64_t kcr_flash_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seqlen_q,
+                                      int64_t head_dim);
+int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                  const kcr_tensor* dout, const kcr_tensor* lse, const kcr_tensor* delta,
+                  const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                  int64_t window_left, int64_t window_right, double softcap,
+                  const kcr_tensor* dq, const kcr_tensor* dk, const kcr_tensor* dv,
+                  void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Varlen backward. replaces `varlen_bwd_explicit` (flash-attn2-rs/src/host/varlen/
+ * backward.rs:15-546) with p_dropout == 0. delta float32 [H, Tq + 128*B] is written
+ * here (the reference computes it inside the same export, backward.rs:323-346). */
+int64_t kcr_flash_varlen_bwd_workspace_bytes(int64_t total_q, int64_t heads, int64_t batch,
+                                             int64_t head_dim);
+int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                         const kcr_tensor* dout, const kcr_tensor* out, const kcr_tensor* lse,
+                         const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
+                         const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                         int64_t window_left, int64_t window_right, double softcap,
+                         int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
+                         const kcr_tensor* dq, const kcr_tensor* dk, const kcr_tensor* dv,
+                         const kcr_tensor* delta, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KCR_HIP_H */

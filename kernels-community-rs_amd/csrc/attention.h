@@ -1,0 +1,151 @@
+// Shared pieces of the FlashAttention-2 kernels (forward and backward):
+// MFMA operand types, the launch parameters, score/mask math and the host-side
+// argument normalisation of flash-attn2-rs/src/host/forward/mod.rs:303-328.
+#pragma once
+
+#include "common.h"
+
+namespace kcr {
+namespace attn {
+
+// ---------------------------------------------------------------------------
+// MFMA 32x32x16 (gfx950). Operand layout (verified on the device):
+//   A (32 x 16): lane l holds A[l % 32][8 * (l / 32) + j], j = 0..7
+//   B (16 x 32): lane l holds B[8 * (l / 32) + j][l % 32]
+//   C (32 x 32): lane l, register r holds C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32]
+// ---------------------------------------------------------------------------
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+using f32x16 = float __attribute__((ext_vector_type(16)));
+
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
+    if constexpr (sizeof(T) == 2 && std::is_same<T, bf16_t>::value) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+}
+
+// Packs two f32 into the element type T (round to nearest even), lo in the low half.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return Elem<T>::from_f32(lo) | (Elem<T>::from_f32(hi) << 16);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Launch parameters shared by the dense and varlen forward kernels. Strides are
+// in elements. Window bounds follow the normalisation of the reference
+// (host/forward/mod.rs:310-328): -1 = unbounded on that side.
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    const float* alibi;
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    const int32_t* seqused_k;
+    const int32_t* leftpad_k;
+    int64_t q_b, q_s, q_h;
+    int64_t k_b, k_s, k_h;
+    int64_t v_b, v_s, v_h;
+    int64_t o_b, o_s, o_h;
+    int64_t lse_b, lse_h;  // dense: [B,H,Sq] -> H*Sq, Sq; varlen: [H,Tq] -> 0, Tq
+    int32_t total_q, total_k;    // varlen: rows of q and k (bounds for cu_seqlens)
+    int32_t batch, heads, kv_heads, gqa;
+    int32_t seqlen_q, seqlen_k;  // dense sizes; varlen: max_seqlen_q / max_seqlen_k
+    int32_t head_dim;            // real head size (<= bucket D)
+    int32_t window_left, window_right;
+    int32_t q_blocks;            // query tiles per (batch, head)
+    int32_t xcd_groups;          // 1: group the query heads of one KV head on one XCD
+    int32_t alibi_b;             // alibi batch stride (0 for [H])
+    int32_t alibi_causal;
+    float scale_log2;            // softmax scale * log2(e), no softcap
+    float tanh_scale;            // softcap: tanh(raw * tanh_scale) * scale_eff
+    float scale_eff_log2;        // softcap: softcap * sign(scale) * log2(e)
+};
+
+// Host-side normalisation of the attention options shared by all entry points.
+struct Options {
+    float scale;
+    float tanh_scale;
+    float scale_eff;
+    int32_t window_left;
+    int32_t window_right;
+    int32_t alibi_causal;
+};
+
+// flash-attn2-rs/src/host/forward/mod.rs:303-328 (and varlen/mod.rs:250-268 with
+// seqlen_k = max_seqlen_k).
+inline Options normalize_options(int has_scale, double scale, int causal, int64_t wl, int64_t wr,
+                                 double softcap, int64_t head_dim, int64_t seqlen_k) {
+    if (wl < INT32_MIN || wl > INT32_MAX || wr < INT32_MIN || wr > INT32_MAX) {
+        throw value_error("window sizes must fit int32");
+    }
+    Options o;
+    const double s = has_scale ? scale : 1.0 / std::sqrt(static_cast<double>(head_dim));
+    if (softcap > 0.0 && s != 0.0) {
+        o.scale = static_cast<float>(std::copysign(softcap, s));
+        o.tanh_scale = static_cast<float>(std::fabs(s) / softcap);
+        o.scale_eff = o.scale;
+    } else {
+        o.scale = static_cast<float>(s);
+        o.tanh_scale = 0.0f;
+        o.scale_eff = static_cast<float>(s);
+    }
+    if (wl >= seqlen_k) wl = -1;
+    if (wr >= seqlen_k) wr = -1;
+    if (causal) wr = 0;
+    o.alibi_causal = (wl < 0 && wr == 0) ? 1 : 0;
+    if (wl < 0 && wr >= 0) wl = seqlen_k;
+    if (wl >= 0 && wr < 0) wr = seqlen_k;
+    o.window_left = static_cast<int32_t>(wl);
+    o.window_right = static_cast<int32_t>(wr);
+    return o;
+}
+
+inline const char* dtype_name(int dtype) {
+    switch (dtype) {
+        case KCR_FLOAT16: return "float16";
+        case KCR_BFLOAT16: return "bfloat16";
+        case KCR_FLOAT32: return "float32";
+        default: return "other";
+    }
+}
+
+// Common tensor checks for q/k/v-like tensors: half precision, unit last stride,
+// 16-byte aligned rows (the kernels move 16-byte vectors).
+inline void check_qkv(const kcr_tensor* t, const char* name, int ndim) {
+    if (!t) throw value_error(std::string(name) + " is required");
+    if (t->ndim != ndim) {
+        throw value_error(std::string(name) + " must have " + std::to_string(ndim) +
+                          " dimensions, got shape " + shape_string(*t));
+    }
+    if (t->dtype != KCR_FLOAT16 && t->dtype != KCR_BFLOAT16) {
+        throw type_error(std::string(name) + " must be float16 or bfloat16, got " +
+                         dtype_name(t->dtype));
+    }
+    if (t->strides[ndim - 1] != 1 && t->shape[ndim - 1] > 1) {
+        throw value_error(std::string(name) + " must have a contiguous last dimension");
+    }
+}
+
+inline bool rows_aligned16(const kcr_tensor* t) {
+    if (!aligned16(t->data)) return false;
+    for (int i = 0; i + 1 < t->ndim; ++i) {
+        if (t->shape[i] > 1 && (t->strides[i] % 8) != 0) return false;
+    }
+    return true;
+}
+
+}  // namespace attn
+}  // namespace kcr

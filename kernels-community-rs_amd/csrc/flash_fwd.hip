@@ -1,0 +1,703 @@
+// FlashAttention-2 forward on MI355X (gfx950): dense (`fwd`, `fwd_lse`) and packed
+// variable-length (`varlen_fwd_explicit`) attention with GQA, causal / sliding
+// windows, softcap and ALiBi.
+//
+// Reference semantics: flash-attn2-rs/src/device/forward/mod.rs:1162-1407 (core
+// loop), :444-557 (scores and masks), :846-871 (LSE), device/config.rs:103-207
+// (launch tile, GQA head mapping, key range), device/varlen/mod.rs:60-210 (per
+// sequence bounds from cu_seqlens), host/forward/mod.rs:52-853 and
+// host/varlen/mod.rs:21-670 (validation, window normalisation, empty inputs).
+//
+// MI355X design
+//   * One block = NW waves; each wave owns 32*QT query rows, so a block covers
+//     BM = 32*QT*NW rows of one (batch, head). Keys stream in tiles of BN = 64.
+//   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16
+//     (bf16 or f16): the accumulator layout puts one query per lane (lane % 32)
+//     and 16 keys per lane-half in registers, so the online-softmax row max is a
+//     register reduction plus ONE cross-half exchange (lane ^ 32), and the row
+//     sum needs no exchange until the end.
+//   * The exponentiated scores are already laid out as the B operand of
+//     O^T = V^T P^T: the accumulator registers are packed to bf16/f16 pairs in
+//     place, no LDS round trip for P.
+//   * Q stays in VGPRs for the whole key loop. K is staged row-major in LDS (one
+//     ds_read_b128 per MFMA operand); V is staged transposed ([d][key], two
+//     ds_read_b64 per operand), the transpose done by the loading threads in
+//     registers (4 keys x 8 d per thread -> eight 8-byte LDS stores).
+//   * The next K/V tile is fetched from HBM into registers while the current tile
+//     is consumed (register double-buffering); masks are evaluated only on tiles
+//     that cross a causal / window / sequence edge.
+//   * Causal grids run the longest query tiles first, and the query heads sharing
+//     one KV head are placed on one XCD (blocks are dealt round-robin over the 8
+//     XCDs) so their K/V tiles hit the same L2.
+#include "attention.h"
+
+namespace kcr {
+namespace attn {
+
+constexpr int kBN = 64;  // keys per tile
+
+template <typename T, int D, int QT, int NW, bool VARLEN, bool GENERAL>
+__global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
+    constexpr int BN = kBN;
+    constexpr int BM = 32 * QT * NW;
+    constexpr int NT = NW * 64;
+    constexpr int KS = D / 16;  // MFMA k-steps over the head dim
+    constexpr int DB = D / 32;  // 32-wide blocks of the head dim in O
+    constexpr int KSTR = D + 8;  // K tile row stride in LDS (elements)
+    constexpr int VSTR = BN + 8;  // V^T tile row stride in LDS (elements)
+    constexpr int DCH = D / 8;  // 16-byte chunks per row
+    constexpr int KCH = BN * DCH;
+    constexpr int KPT = (KCH + NT - 1) / NT;
+    constexpr int VIT = (BN / 4) * DCH;
+    constexpr int VPT = (VIT + NT - 1) / NT;
+
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * KSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * VSTR];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;
+
+    // ---- block -> (batch, head, query tile) ----
+    const int per_tile = p.batch * p.heads;
+    const int qo = blockIdx.x / per_tile;
+    const int rem = blockIdx.x - qo * per_tile;
+    int bh;
+    if (p.xcd_groups) {
+        const int xcd = rem & 7;
+        const int rr = rem >> 3;
+        const int j = rr % p.gqa;
+        const int g = (rr / p.gqa) * 8 + xcd;
+        bh = g * p.gqa + j;
+    } else {
+        bh = rem;
+    }
+    const int b = bh / p.heads;
+    const int head = bh - b * p.heads;
+    const int kvh = head / p.gqa;
+    const int qb = p.q_blocks - 1 - qo;  // longest causal tiles first
+
+    int64_t q_off = 0, k_off = 0;
+    int sq = p.seqlen_q, sk = p.seqlen_k;
+    int lse_row0 = 0;
+    if constexpr (VARLEN) {
+        const int qs = p.cu_q[b];
+        const int qe = p.cu_q[b + 1];
+        const int ks = p.cu_k[b];
+        const int ke = p.cu_k[b + 1];
+        const int len = p.seqused_k ? p.seqused_k[b] : ke - ks;
+        const int pad = p.leftpad_k ? p.leftpad_k[b] : 0;
+        // Metadata is trusted as in the reference; only memory bounds are guarded.
+        if (qs < 0 || qe < qs || qe > p.total_q || ks < 0 || ke < ks || ke > p.total_k || pad < 0 ||
+            len < pad || len > ke - ks || qe - qs > p.seqlen_q) {
+            return;
+        }
+        sq = qe - qs;
+        sk = len - pad;
+        q_off = static_cast<int64_t>(qs);
+        k_off = static_cast<int64_t>(ks + pad);
+        lse_row0 = qs;
+    }
+    const int row0 = qb * BM;
+    if (row0 >= sq) return;
+    const int off = sk - sq;
+    const int wl = p.window_left;
+    const int wr = p.window_right;
+
+    const uint16_t* qbase;
+    const uint16_t* kbase;
+    const uint16_t* vbase;
+    uint16_t* obase;
+    if constexpr (VARLEN) {
+        qbase = static_cast<const uint16_t*>(p.q) + q_off * p.q_s + head * p.q_h;
+        kbase = static_cast<const uint16_t*>(p.k) + k_off * p.k_s + kvh * p.k_h;
+        vbase = static_cast<const uint16_t*>(p.v) + k_off * p.v_s + kvh * p.v_h;
+        obase = static_cast<uint16_t*>(p.o) + q_off * p.o_s + head * p.o_h;
+    } else {
+        qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
+        kbase = static_cast<const uint16_t*>(p.k) + b * p.k_b + kvh * p.k_h;
+        vbase = static_cast<const uint16_t*>(p.v) + b * p.v_b + kvh * p.v_h;
+        obase = static_cast<uint16_t*>(p.o) + b * p.o_b + head * p.o_h;
+    }
+    float* lse_base = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + lse_row0;
+
+    // ---- key range of this query tile (device/config.rs:183-207) ----
+    const int last_row = min(row0 + BM, sq) - 1;
+    int kv_end = sk;
+    if (wr >= 0) kv_end = max(0, min(sk, last_row + 1 + off + wr));
+    int kv_begin = 0;
+    if (wl >= 0) kv_begin = (max(0, min(sk, row0 + off - wl)) / BN) * BN;
+
+    // ---- Q fragments in registers: B operand of S^T = K Q^T ----
+    const int wrow0 = row0 + wave * 32 * QT;
+    u32x4 qf[QT][KS];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int row = wrow0 + qt * 32 + l32;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = 16 * ks + 8 * hh;
+            if (row < sq && d0 < p.head_dim) {
+                qf[qt][ks] = *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + d0);
+            } else {
+                qf[qt][ks] = u32x4{0, 0, 0, 0};
+            }
+        }
+    }
+
+    float slope_log2 = 0.0f;
+    if constexpr (GENERAL) {
+        if (p.alibi) slope_log2 = p.alibi[b * p.alibi_b + head] * kLog2e;
+    }
+
+    f32x16 o[QT][DB];
+    float m[QT], l[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[qt][db] = f32x16{};
+    }
+
+    // ---- tile staging: HBM -> registers -> LDS ----
+    u32x4 kreg[KPT];
+    u32x4 vreg[VPT][4];
+    auto load_tile = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + i * NT;
+            kreg[i] = u32x4{0, 0, 0, 0};
+            if (c < KCH) {
+                const int key = c / DCH;
+                const int dc = c - key * DCH;
+                const int gk = kb + key;
+                if (gk < sk && dc * 8 < p.head_dim) {
+                    kreg[i] = *reinterpret_cast<const u32x4*>(kbase + gk * p.k_s + dc * 8);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int it = tid + i * NT;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vreg[i][e] = u32x4{0, 0, 0, 0};
+            if (it < VIT) {
+                const int kq = it / DCH;
+                const int dc = it - kq * DCH;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int gk = kb + 4 * kq + e;
+                    if (gk < sk && dc * 8 < p.head_dim) {
+                        vreg[i][e] = *reinterpret_cast<const u32x4*>(vbase + gk * p.v_s + dc * 8);
+                    }
+                }
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + i * NT;
+            if (c < KCH) {
+                const int key = c / DCH;
+                const int dc = c - key * DCH;
+                *reinterpret_cast<u32x4*>(&k_lds[key * KSTR + dc * 8]) = kreg[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int it = tid + i * NT;
+            if (it < VIT) {
+                const int kq = it / DCH;
+                const int dc = it - kq * DCH;
+#pragma unroll
+                for (int dd = 0; dd < 8; ++dd) {
+                    const int w = dd >> 1;
+                    const int sh = (dd & 1) * 16;
+                    const uint32_t e0 = (vreg[i][0][w] >> sh) & 0xffffu;
+                    const uint32_t e1 = (vreg[i][1][w] >> sh) & 0xffffu;
+                    const uint32_t e2 = (vreg[i][2][w] >> sh) & 0xffffu;
+                    const uint32_t e3 = (vreg[i][3][w] >> sh) & 0xffffu;
+                    uint2 packed;
+                    packed.x = e0 | (e1 << 16);
+                    packed.y = e2 | (e3 << 16);
+                    *reinterpret_cast<uint2*>(&v_lds[(8 * dc + dd) * VSTR + 4 * kq]) = packed;
+                }
+            }
+        }
+    };
+
+    if (kv_begin < kv_end) {
+        load_tile(kv_begin);
+        store_tile();
+        __syncthreads();
+    }
+
+    for (int kb = kv_begin; kb < kv_end; kb += BN) {
+        const bool has_next = kb + BN < kv_end;
+        if (has_next) load_tile(kb + BN);
+
+        // ---- S^T = K Q^T for 64 keys x 32*QT queries ----
+        f32x16 s[QT][2];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            s[qt][0] = f32x16{};
+            s[qt][1] = f32x16{};
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(&k_lds[l32 * KSTR + 16 * ks + 8 * hh]);
+            const u32x4 ka1 =
+                *reinterpret_cast<const u32x4*>(&k_lds[(32 + l32) * KSTR + 16 * ks + 8 * hh]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                s[qt][0] = mfma32<T>(ka0, qf[qt][ks], s[qt][0]);
+                s[qt][1] = mfma32<T>(ka1, qf[qt][ks], s[qt][1]);
+            }
+        }
+
+        // ---- scores (log2 domain), masks, online softmax ----
+        const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
+                               (wl >= 0 && kb < last_row + off - wl);
+        u32x4 pk[QT][4];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const int row = wrow0 + qt * 32 + l32;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float x = s[qt][sub][r];
+                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if constexpr (GENERAL) {
+                        if (p.tanh_scale > 0.0f) {
+                            x = tanhf(x * p.tanh_scale) * p.scale_eff_log2;
+                        } else {
+                            x *= p.scale_log2;
+                        }
+                        if (p.alibi) {
+                            x += p.alibi_causal ? slope_log2 * static_cast<float>(col)
+                                                : -slope_log2 * fabsf(static_cast<float>(row + off - col));
+                        }
+                    } else {
+                        x *= p.scale_log2;
+                    }
+                    if (need_mask) {
+                        const bool masked = (col >= sk) || (wr >= 0 && col > row + off + wr) ||
+                                            (wl >= 0 && col < row + off - wl);
+                        if (masked) x = -INFINITY;
+                    }
+                    s[qt][sub][r] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m[qt], mx);
+            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+            const float alpha = fast_exp2(m[qt] - m_use);
+            m[qt] = m_new;
+            float rowsum = 0.0f;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = fast_exp2(s[qt][sub][r] - m_use);
+                    s[qt][sub][r] = pv;
+                    rowsum += pv;
+                }
+            }
+            l[qt] = l[qt] * alpha + rowsum;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[qt][db] *= alpha;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int sub = t >> 1;
+                const int base = 8 * (t & 1);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    pk[qt][t][w] = pack2<T>(s[qt][sub][base + 2 * w], s[qt][sub][base + 2 * w + 1]);
+                }
+            }
+        }
+
+        // ---- O^T += V^T P^T ----
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint16_t* vrow = &v_lds[(32 * db + l32) * VSTR + 16 * t + 4 * hh];
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+                const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][db] = mfma32<T>(va, pk[qt][t], o[qt][db]);
+            }
+        }
+
+        __syncthreads();
+        if (has_next) {
+            store_tile();
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue: O / l, LSE = (m + log2 l) * ln 2 (forward/mod.rs:846-865) ----
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int row = wrow0 + qt * 32 + l32;
+        const float lt = l[qt] + __shfl_xor(l[qt], 32, 64);
+        if (row >= sq) continue;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        uint16_t* orow = obase + row * p.o_s;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * hh;
+                if (d < p.head_dim) {
+                    uint2 w;
+                    w.x = pack2<T>(o[qt][db][4 * g] * inv, o[qt][db][4 * g + 1] * inv);
+                    w.y = pack2<T>(o[qt][db][4 * g + 2] * inv, o[qt][db][4 * g + 3] * inv);
+                    *reinterpret_cast<uint2*>(orow + d) = w;
+                }
+            }
+        }
+        if (hh == 0) lse_base[row] = lt > 0.0f ? (m[qt] + fast_log2(lt)) * kLn2 : INFINITY;
+    }
+}
+
+// Empty-key rows: O = 0, LSE = +inf (host/forward/mod.rs:548-572). Also clears
+// the output when zero_tensors is requested. Uses kernels rather than
+// hipMemsetAsync so the calls stay safe inside captured graphs.
+__global__ void fill_rows_kernel(uint16_t* o, int64_t o_rows, int64_t row_stride_tokens,
+                                 int64_t row_elems, int64_t o_row_stride) {
+    (void)row_stride_tokens;
+    const int64_t total = o_rows * row_elems;
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += gridDim.x * 256ll) {
+        const int64_t r = i / row_elems;
+        const int64_t c = i - r * row_elems;
+        o[r * o_row_stride + c] = 0;
+    }
+}
+
+__global__ void fill_f32_kernel(float* x, int64_t n, float value) {
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) x[i] = value;
+}
+
+}  // namespace attn
+
+namespace {
+
+using namespace attn;
+
+void fill_f32(float* x, int64_t n, float value, hipStream_t s) {
+    if (n <= 0) return;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
+    fill_f32_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(x, n, value);
+    check_launch("fill lse");
+}
+
+// Zeroes a [rows, cols] view of 16-bit elements with a given row stride.
+void zero_rows(void* o, int64_t rows, int64_t cols, int64_t row_stride, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return;
+    const int64_t blocks = std::min<int64_t>((rows * cols + 255) / 256, 65536);
+    fill_rows_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<uint16_t*>(o), rows,
+                                                                  0, cols, row_stride);
+    check_launch("zero output");
+}
+
+struct Config {
+    int qt;
+    int nw;
+};
+
+// Tile configuration per head-dim bucket.
+Config config_for(int D) {
+    (void)D;
+    return Config{1, 4};
+}
+
+template <typename T, int D, int QT, int NW, bool VARLEN>
+void launch_cfg(FwdParams& prm, bool general, hipStream_t s) {
+    constexpr int BM = 32 * QT * NW;
+    prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
+    const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads;
+    if (blocks == 0) return;
+    if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
+    prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
+    if (general) {
+        flash_fwd_kernel<T, D, QT, NW, VARLEN, true><<<static_cast<unsigned>(blocks), NW * 64, 0, s>>>(prm);
+    } else {
+        flash_fwd_kernel<T, D, QT, NW, VARLEN, false><<<static_cast<unsigned>(blocks), NW * 64, 0, s>>>(prm);
+    }
+    check_launch("launch flash_fwd");
+}
+
+template <typename T, int D, bool VARLEN>
+void launch_d(FwdParams& prm, bool general, hipStream_t s) {
+    launch_cfg<T, D, 1, 4, VARLEN>(prm, general, s);
+}
+
+template <bool VARLEN>
+void launch_fwd(FwdParams& prm, int dtype, int bucket, bool general, hipStream_t s) {
+    auto by_d = [&](auto tag) {
+        using T = decltype(tag);
+        switch (bucket) {
+            case 32: launch_d<T, 32, VARLEN>(prm, general, s); break;
+            case 64: launch_d<T, 64, VARLEN>(prm, general, s); break;
+            case 96: launch_d<T, 96, VARLEN>(prm, general, s); break;
+            case 128: launch_d<T, 128, VARLEN>(prm, general, s); break;
+            case 160: launch_d<T, 160, VARLEN>(prm, general, s); break;
+            case 192: launch_d<T, 192, VARLEN>(prm, general, s); break;
+            case 224: launch_d<T, 224, VARLEN>(prm, general, s); break;
+            case 256: launch_d<T, 256, VARLEN>(prm, general, s); break;
+            default: throw value_error("unsupported head dim bucket " + std::to_string(bucket));
+        }
+    };
+    if (dtype == KCR_BFLOAT16) {
+        by_d(bf16_t{});
+    } else {
+        by_d(f16_t{});
+    }
+}
+
+int bucket_for(int64_t d) { return static_cast<int>((d + 31) / 32 * 32); }
+
+void check_alibi(const kcr_tensor* alibi, int64_t b, int64_t h, int32_t& alibi_b) {
+    alibi_b = 0;
+    if (!alibi) return;
+    if (alibi->dtype != KCR_FLOAT32) throw type_error("alibi_slopes must be float32");
+    if (!is_contiguous(*alibi)) throw value_error("alibi_slopes must be contiguous");
+    if (alibi->ndim == 1 && alibi->shape[0] == h) {
+        alibi_b = 0;
+    } else if (alibi->ndim == 2 && alibi->shape[0] == b && alibi->shape[1] == h) {
+        alibi_b = static_cast<int32_t>(h);
+    } else {
+        throw value_error("alibi_slopes must be [" + std::to_string(h) + "] or [" +
+                          std::to_string(b) + ", " + std::to_string(h) + "]");
+    }
+    require_device(alibi, "alibi_slopes");
+}
+
+void check_head_dim(int64_t d) {
+    if (d > 256) throw value_error("head dim must be <= 256, got " + std::to_string(d));
+    if (d < 8 || d % 8 != 0) {
+        throw value_error("head_size must be a positive multiple of 8 (like the reference), got " +
+                          std::to_string(d));
+    }
+}
+
+}  // namespace
+}  // namespace kcr
+
+using namespace kcr;
+using namespace kcr::attn;
+
+extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                             const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                             int64_t window_left, int64_t window_right, double softcap,
+                             const kcr_tensor* out, const kcr_tensor* lse, void* stream) {
+    return guarded([&] {
+        check_qkv(q, "q", 4);
+        check_qkv(k, "k", 4);
+        check_qkv(v, "v", 4);
+        if (k->dtype != q->dtype || v->dtype != q->dtype) {
+            throw type_error("q, k, v must share dtype (all f16 or all bf16)");
+        }
+        const int64_t B = q->shape[0], Sq = q->shape[1], H = q->shape[2], D = q->shape[3];
+        const int64_t Sk = k->shape[1], Hk = k->shape[2];
+        if (k->shape[0] != B || k->shape[3] != D) {
+            throw value_error("k must be [B, Sk, Hk, D] with q's batch and head dim");
+        }
+        if (shape_of(*v) != shape_of(*k)) throw value_error("v must have k's shape [B, Sk, Hk, D]");
+        check_head_dim(D);
+        if (Hk <= 0 || H % Hk != 0) {
+            throw value_error("num_heads (" + std::to_string(H) + ") must be a multiple of num_heads_k (" +
+                              std::to_string(Hk) + ")");
+        }
+        if (B <= 0 || H <= 0 || B > 65535 || H > 65535) {
+            throw value_error("batch and heads must each be in 1..=65535, got " + std::to_string(B) +
+                              " and " + std::to_string(H));
+        }
+        if (Sq > INT32_MAX - 256 || Sk > INT32_MAX - 256) {
+            throw value_error("sequence lengths must fit int32");
+        }
+        int32_t alibi_b = 0;
+        check_alibi(alibi, B, H, alibi_b);
+        if (!out || shape_of(*out) != shape_of(*q) || out->dtype != q->dtype) {
+            throw value_error("out must match q's shape, dtype and device");
+        }
+        if (out->strides[3] != 1) throw value_error("out must have unit last stride");
+        if (!lse || lse->dtype != KCR_FLOAT32 || lse->ndim != 3 || lse->shape[0] != B ||
+            lse->shape[1] != H || lse->shape[2] != Sq || !is_contiguous(*lse)) {
+            throw value_error("lse must be contiguous float32 [B, H, Sq]");
+        }
+        for (auto* t : {q, k, v, out}) {
+            if (!rows_aligned16(t)) {
+                throw value_error("q, k, v and out must have 16-byte aligned rows (strides multiple of 8 elements)");
+            }
+        }
+        require_device(q, "q");
+        require_device(k, "k");
+        require_device(v, "v");
+        require_device(out, "out");
+        require_device(lse, "lse");
+        auto s = static_cast<hipStream_t>(stream);
+        const Options opt = normalize_options(has_scale, scale, causal, window_left, window_right,
+                                              softcap, D, Sk);
+        if (Sq == 0) return;
+        if (Sk == 0) {
+            // Every row is empty: O = 0, LSE = +inf.
+            for (int64_t bi = 0; bi < B; ++bi) {
+                auto* base = static_cast<uint16_t*>(out->data) + bi * out->strides[0];
+                for (int64_t hi = 0; hi < H; ++hi) {
+                    zero_rows(base + hi * out->strides[2], Sq, D, out->strides[1], s);
+                }
+            }
+            fill_f32(static_cast<float*>(lse->data), B * H * Sq, INFINITY, s);
+            return;
+        }
+        FwdParams prm{};
+        prm.q = q->data;
+        prm.k = k->data;
+        prm.v = v->data;
+        prm.o = out->data;
+        prm.lse = static_cast<float*>(lse->data);
+        prm.alibi = alibi ? static_cast<const float*>(alibi->data) : nullptr;
+        prm.q_b = q->strides[0]; prm.q_s = q->strides[1]; prm.q_h = q->strides[2];
+        prm.k_b = k->strides[0]; prm.k_s = k->strides[1]; prm.k_h = k->strides[2];
+        prm.v_b = v->strides[0]; prm.v_s = v->strides[1]; prm.v_h = v->strides[2];
+        prm.o_b = out->strides[0]; prm.o_s = out->strides[1]; prm.o_h = out->strides[2];
+        prm.lse_b = H * Sq;
+        prm.lse_h = Sq;
+        prm.batch = static_cast<int32_t>(B);
+        prm.heads = static_cast<int32_t>(H);
+        prm.kv_heads = static_cast<int32_t>(Hk);
+        prm.gqa = static_cast<int32_t>(H / Hk);
+        prm.seqlen_q = static_cast<int32_t>(Sq);
+        prm.seqlen_k = static_cast<int32_t>(Sk);
+        prm.head_dim = static_cast<int32_t>(D);
+        prm.window_left = opt.window_left;
+        prm.window_right = opt.window_right;
+        prm.alibi_b = alibi_b;
+        prm.alibi_causal = opt.alibi_causal;
+        prm.scale_log2 = opt.scale * kLog2e;
+        prm.tanh_scale = opt.tanh_scale;
+        prm.scale_eff_log2 = opt.scale_eff * kLog2e;
+        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr;
+        launch_fwd<false>(prm, q->dtype, bucket_for(D), general, s);
+    });
+}
+
+extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                                    const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
+                                    const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
+                                    const kcr_tensor* alibi, int has_scale, double scale,
+                                    int causal, int64_t window_left, int64_t window_right,
+                                    double softcap, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                    int zero_tensors, const kcr_tensor* out,
+                                    const kcr_tensor* lse, void* stream) {
+    return guarded([&] {
+        check_qkv(q, "q", 3);
+        check_qkv(k, "k", 3);
+        check_qkv(v, "v", 3);
+        if (k->dtype != q->dtype || v->dtype != q->dtype || shape_of(*k) != shape_of(*v) ||
+            k->shape[2] != q->shape[2]) {
+            throw value_error("inconsistent packed attention inputs");
+        }
+        if (!cu_seqlens_q || cu_seqlens_q->ndim != 1 || cu_seqlens_q->shape[0] < 2) {
+            throw value_error("cu_seqlens_q must have shape [batch + 1]");
+        }
+        const int64_t batch = cu_seqlens_q->shape[0] - 1;
+        const int64_t Tq = q->shape[0], H = q->shape[1], D = q->shape[2];
+        const int64_t Tk = k->shape[0], Hk = k->shape[1];
+        check_head_dim(D);
+        if (batch <= 0 || H <= 0 || Hk <= 0 || H % Hk != 0 || batch > 65535 || H > 65535 ||
+            Tq > INT32_MAX || Tk > INT32_MAX || max_seqlen_q < 0 || max_seqlen_k < 0 ||
+            max_seqlen_q > INT32_MAX - 256 || max_seqlen_k > INT32_MAX - 256) {
+            throw value_error("unsupported packed attention dimensions");
+        }
+        auto check_meta = [&](const kcr_tensor* t, int64_t n, const char* name) {
+            if (!t) return;
+            if (t->dtype != KCR_INT32 || t->ndim != 1 || t->shape[0] != n || !is_contiguous(*t)) {
+                throw value_error(std::string(name) + " must be contiguous int32 [" + std::to_string(n) + "]");
+            }
+            require_device(t, name);
+        };
+        if (!cu_seqlens_k) throw value_error("cu_seqlens_k is required");
+        check_meta(cu_seqlens_q, batch + 1, "cu_seqlens_q");
+        check_meta(cu_seqlens_k, batch + 1, "cu_seqlens_k");
+        check_meta(seqused_k, batch, "seqused_k");
+        check_meta(leftpad_k, batch, "leftpad_k");
+        int32_t alibi_b = 0;
+        check_alibi(alibi, batch, H, alibi_b);
+        if (!out || shape_of(*out) != shape_of(*q) || out->dtype != q->dtype || out->strides[2] != 1) {
+            throw value_error("out must match q's shape and dtype with unit last stride");
+        }
+        if (!lse || lse->dtype != KCR_FLOAT32 || lse->ndim != 2 || lse->shape[0] != H ||
+            lse->shape[1] != Tq || !is_contiguous(*lse)) {
+            throw value_error("lse must be contiguous float32 [H, total_q]");
+        }
+        for (auto* t : {q, k, v, out}) {
+            if (Tq > 0 && !rows_aligned16(t)) {
+                throw value_error("q, k, v and out must have 16-byte aligned rows (strides multiple of 8 elements)");
+            }
+        }
+        require_device(q, "q");
+        require_device(k, "k");
+        require_device(v, "v");
+        require_device(out, "out");
+        require_device(lse, "lse");
+        auto s = static_cast<hipStream_t>(stream);
+        // varlen/mod.rs:250-268: single-query packs drop causality; windows use max_k.
+        int causal_eff = causal;
+        if (max_seqlen_q == 1 && !alibi) causal_eff = 0;
+        const Options opt = normalize_options(has_scale, scale, causal_eff, window_left, window_right,
+                                              softcap, D, max_seqlen_k);
+        if (zero_tensors || max_seqlen_k == 0) {
+            // varlen/mod.rs:418-443: cleared output, LSE -inf (+inf without keys).
+            zero_rows(out->data, Tq, H * D, out->strides[0], s);
+            fill_f32(static_cast<float*>(lse->data), H * Tq, max_seqlen_k == 0 ? INFINITY : -INFINITY, s);
+        }
+        if (Tq == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) return;
+        FwdParams prm{};
+        prm.q = q->data;
+        prm.k = k->data;
+        prm.v = v->data;
+        prm.o = out->data;
+        prm.lse = static_cast<float*>(lse->data);
+        prm.alibi = alibi ? static_cast<const float*>(alibi->data) : nullptr;
+        prm.cu_q = static_cast<const int32_t*>(cu_seqlens_q->data);
+        prm.cu_k = static_cast<const int32_t*>(cu_seqlens_k->data);
+        prm.total_q = static_cast<int32_t>(Tq);
+        prm.total_k = static_cast<int32_t>(Tk);
+        prm.seqused_k = seqused_k ? static_cast<const int32_t*>(seqused_k->data) : nullptr;
+        prm.leftpad_k = leftpad_k ? static_cast<const int32_t*>(leftpad_k->data) : nullptr;
+        prm.q_s = q->strides[0]; prm.q_h = q->strides[1];
+        prm.k_s = k->strides[0]; prm.k_h = k->strides[1];
+        prm.v_s = v->strides[0]; prm.v_h = v->strides[1];
+        prm.o_s = out->strides[0]; prm.o_h = out->strides[1];
+        prm.lse_b = 0;
+        prm.lse_h = Tq;
+        prm.batch = static_cast<int32_t>(batch);
+        prm.heads = static_cast<int32_t>(H);
+        prm.kv_heads = static_cast<int32_t>(Hk);
+        prm.gqa = static_cast<int32_t>(H / Hk);
+        prm.seqlen_q = static_cast<int32_t>(max_seqlen_q);
+        prm.seqlen_k = static_cast<int32_t>(max_seqlen_k);
+        prm.head_dim = static_cast<int32_t>(D);
+        prm.window_left = opt.window_left;
+        prm.window_right = opt.window_right;
+        prm.alibi_b = alibi_b;
+        prm.alibi_causal = opt.alibi_causal;
+        prm.scale_log2 = opt.scale * kLog2e;
+        prm.tanh_scale = opt.tanh_scale;
+        prm.scale_eff_log2 = opt.scale_eff * kLog2e;
+        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr;
+        launch_fwd<true>(prm, q->dtype, bucket_for(D), general, s);
+    });
+}

@@ -1,0 +1,555 @@
+// RMSNorm forward, backward and weight-gradient reduction (rmsnorm crate).
+//
+// Reference: rmsnorm/src/device.rs:75-358 (kernels), rmsnorm/src/ops.rs:1-444
+// (validation, dispatch, exports), rmsnorm/src/casting.rs:29-60 (casting modes).
+//
+// MI355X design (forward): rows up to 16 x 16 bytes per lane (8192 bf16 / 4096 f32
+// columns) take a one-pass wave-per-row kernel. Each 64-lane wave loads its whole
+// row into VGPRs with 16-byte loads, reduces the sum of squares with a wave64
+// butterfly (no LDS, no barrier), and normalises straight from registers, so x is
+// read from HBM exactly once and y written once. The weight row is loaded into
+// registers once per wave and reused for every row the wave visits. Wider or
+// misaligned rows take a block-per-row kernel that makes a second pass over the
+// row (served from L2) like the reference.
+//
+// Backward: blocks own contiguous row ranges (one row of f32 partial weight
+// gradients per block, as the reference's `dw_partial`), reduced by
+// `reduce_weight_grad` in a fixed order.
+#include "common.h"
+
+namespace kcr {
+
+enum Mode : int { MODE_LLAMA = 0, MODE_GEMMA = 1, MODE_NONE = 2 };
+
+// Casting-mode flags of rmsnorm/src/casting.rs:44-60.
+template <int M>
+struct Casting {
+    static constexpr bool input_dtype_math = (M == MODE_NONE);
+    static constexpr bool round_x_hat = (M != MODE_GEMMA);
+    static constexpr bool round_weight_grad = (M == MODE_LLAMA);
+};
+
+template <typename T>
+__device__ __forceinline__ float rnd(float v) {
+    return Elem<T>::round(v);
+}
+
+template <typename T>
+constexpr int vec_of() {
+    return 16 / sizeof(typename Elem<T>::storage);
+}
+
+// 16 bytes of T (8 x 16-bit or 4 x f32) widened into f[0..VEC).
+template <typename T>
+__device__ __forceinline__ void widen16(const u32x4& w, float* f) {
+    if constexpr (sizeof(typename Elem<T>::storage) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = Elem<T>::to_f32(w[i] & 0xffffu);
+            f[2 * i + 1] = Elem<T>::to_f32(w[i] >> 16);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 narrow16(const float* f) {
+    u32x4 w;
+    if constexpr (sizeof(typename Elem<T>::storage) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(f[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = Elem<T>::from_f32(f[2 * i]) | (Elem<T>::from_f32(f[2 * i + 1]) << 16);
+    }
+    return w;
+}
+
+// rstd = 1 / sqrt(mean(x^2) + eps), device.rs:147-153.
+template <typename X, int M>
+__device__ __forceinline__ float row_rstd(float sum_sq, float inv_n, float eps) {
+    const float mean_square = sum_sq * inv_n;
+    if constexpr (Casting<M>::input_dtype_math) {
+        return rnd<X>(1.0f / sqrtf(rnd<X>(mean_square) + rnd<X>(eps)));
+    } else {
+        return 1.0f / sqrtf(mean_square + eps);
+    }
+}
+
+// y = x_hat * (offset + w), device.rs:161-179.
+template <typename X, typename W, int M, bool AFFINE>
+__device__ __forceinline__ float normalize(float x, float w, float rstd, float offset) {
+    const float xr = x * rstd;
+    const float x_hat = Casting<M>::round_x_hat ? rnd<X>(xr) : xr;
+    if constexpr (!AFFINE) {
+        return x_hat;
+    } else {
+        const float factor =
+            Casting<M>::input_dtype_math ? rnd<W>(rnd<X>(offset) + w) : offset + w;
+        return x_hat * factor;
+    }
+}
+
+constexpr int kWaves = 4;  // waves per block of the wave-per-row kernel
+
+// One wave per row, the row held in registers: CHUNKS 16-byte vectors per lane.
+// Requires n % VEC_X == 0, 16-byte aligned tensors, and (with AFFINE) a weight
+// whose 16-byte vectors cover the same columns: W == X, or f32 weight read as
+// two 16-byte halves per x vector.
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
+__global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
+    u32x4* __restrict__ y, float* __restrict__ rstd_out, const u32x4* __restrict__ x,
+    const u32x4* __restrict__ weight, uint32_t rows, uint32_t nvec, float inv_n, float eps,
+    float offset) {
+    constexpr int VEC = vec_of<X>();
+    // f32 weight with 16-bit x: two 16-byte weight vectors per x vector.
+    constexpr int WPV = (sizeof(typename Elem<W>::storage) > sizeof(typename Elem<X>::storage)) ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const uint32_t waves = gridDim.x * kWaves;
+
+    u32x4 wv[AFFINE ? CHUNKS * WPV : 1];
+    if constexpr (AFFINE) {
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+#pragma unroll
+            for (int h = 0; h < WPV; ++h) {
+                if (v < nvec) wv[c * WPV + h] = weight[v * WPV + h];
+            }
+        }
+    }
+
+    for (uint32_t row = wave; row < rows; row += waves) {
+        const u32x4* xr = x + static_cast<uint64_t>(row) * nvec;
+        u32x4 xv[CHUNKS];
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) xv[c] = __builtin_nontemporal_load(xr + v);
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) {
+                float f[VEC];
+                widen16<X>(xv[c], f);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) sum += f[e] * f[e];
+            }
+        }
+        sum = wave_sum(sum);
+        const float rstd = row_rstd<X, M>(sum, inv_n, eps);
+        if (lane == 0) rstd_out[row] = rstd;
+        u32x4* yr = y + static_cast<uint64_t>(row) * nvec;
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) {
+                float f[VEC], w[VEC], o[VEC];
+                widen16<X>(xv[c], f);
+                if constexpr (AFFINE) {
+                    if constexpr (WPV == 2) {
+                        widen16<float>(wv[2 * c], w);
+                        widen16<float>(wv[2 * c + 1], w + 4);
+                    } else {
+                        widen16<W>(wv[c], w);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < VEC; ++e)
+                    o[e] = normalize<X, W, M, AFFINE>(f[e], AFFINE ? w[e] : 0.0f, rstd, offset);
+                __builtin_nontemporal_store(narrow16<X>(o), yr + v);
+            }
+        }
+    }
+}
+
+// Block per row, scalar columns; two passes (the second mostly from L2).
+template <typename X, typename W, int M, bool AFFINE>
+__global__ void __launch_bounds__(1024) rms_fwd_block(X* __restrict__ y, float* __restrict__ rstd_out,
+                                                      const X* __restrict__ x,
+                                                      const W* __restrict__ weight, uint32_t n,
+                                                      float inv_n, float eps, float offset) {
+    __shared__ float partial[16];
+    const uint64_t row = blockIdx.x;
+    const X* xr = x + row * n;
+    X* yr = y + row * n;
+    float sum = 0.0f;
+    for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) {
+        const float v = Elem<X>::load(xr + c);
+        sum += v * v;
+    }
+    sum = wave_sum(sum);
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) partial[wid] = sum;
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    float total = (threadIdx.x & 63) < nw ? partial[threadIdx.x & 63] : 0.0f;
+    total = wave_sum(total);
+    const float rstd = row_rstd<X, M>(total, inv_n, eps);
+    if (threadIdx.x == 0) rstd_out[row] = rstd;
+    for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) {
+        const float w = AFFINE ? Elem<W>::load(weight + c) : 0.0f;
+        Elem<X>::store(yr + c, normalize<X, W, M, AFFINE>(Elem<X>::load(xr + c), w, rstd, offset));
+    }
+}
+
+// Gradients of the forward pass, device.rs:228-335:
+//   m  = dy * (offset + w);  dx = rstd * m + rstd * (-(rstd^2 / n) * dot(m, x) * x)
+//   dw_partial[block, :] = sum over the block's rows of dy * x_hat
+template <typename X, typename W, int M, bool AFFINE>
+__global__ void __launch_bounds__(1024) rms_bwd_block(X* dx, float* __restrict__ dw_partial,
+                                                      const X* dy, const X* __restrict__ x,
+                                                      const W* __restrict__ weight,
+                                                      const float* __restrict__ rstd,
+                                                      uint32_t rows, uint32_t n, float inv_n,
+                                                      float offset) {
+    __shared__ float partial[16];
+    const uint32_t per_block = (rows + gridDim.x - 1) / gridDim.x;
+    uint32_t row = blockIdx.x * per_block;
+    const uint32_t row_end = min(row + per_block, rows);
+    float* dw_row = dw_partial + static_cast<uint64_t>(blockIdx.x) * n;
+    if constexpr (AFFINE) {
+        for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) dw_row[c] = 0.0f;
+    }
+    const int nw = blockDim.x >> 6;
+    for (; row < row_end; ++row) {
+        const uint64_t base = static_cast<uint64_t>(row) * n;
+        const float r = rstd[row];
+        float dot = 0.0f;
+        for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) {
+            float g = Elem<X>::load(dy + base + c);
+            if constexpr (AFFINE) g *= Elem<W>::load(weight + c) + offset;
+            dot += g * Elem<X>::load(x + base + c);
+        }
+        dot = wave_sum(dot);
+        if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = dot;
+        __syncthreads();
+        float total = (threadIdx.x & 63) < nw ? partial[threadIdx.x & 63] : 0.0f;
+        total = wave_sum(total);
+        const float correction = -inv_n * r * r * total;
+        for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) {
+            const float g0 = Elem<X>::load(dy + base + c);
+            const float xv = Elem<X>::load(x + base + c);
+            float g = g0;
+            if constexpr (AFFINE) g *= Elem<W>::load(weight + c) + offset;
+            Elem<X>::store(dx + base + c, r * g + r * (correction * xv));
+            if constexpr (AFFINE) {
+                const bool rw = Casting<M>::round_weight_grad;
+                const float x_hat = rw ? rnd<X>(xv * r) : xv * r;
+                const float contrib = rw ? rnd<X>(g0 * x_hat) : g0 * x_hat;
+                dw_row[c] += contrib;
+            }
+        }
+        // The next row reuses `partial`.
+        __syncthreads();
+    }
+}
+
+// dw[c] = sum_b dw_partial[b, c] in a fixed order, rounded to W (device.rs:339-358).
+template <typename W>
+__global__ void __launch_bounds__(256) reduce_weight_grad(W* __restrict__ dw,
+                                                          const float* __restrict__ dw_partial,
+                                                          uint32_t blocks, uint32_t n) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= n) return;
+    float sum = 0.0f;
+    for (uint32_t b = 0; b < blocks; ++b) sum += dw_partial[static_cast<uint64_t>(b) * n + c];
+    Elem<W>::store(dw + c, sum);
+}
+
+namespace {
+
+constexpr int64_t kMaxCols = 65536;
+constexpr int64_t kMaxGridX = 2147483647;
+
+int parse_mode(const char* name) {
+    const std::string s = name ? name : "";
+    if (s == "llama") return MODE_LLAMA;
+    if (s == "gemma") return MODE_GEMMA;
+    if (s == "none") return MODE_NONE;
+    throw value_error("invalid casting mode \"" + s +
+                      "\", expected \"llama\", \"gemma\" or \"none\"");
+}
+
+// rows_and_cols of rmsnorm/src/ops.rs:57-74.
+void rows_and_cols(const kcr_tensor* x, int64_t& rows, int64_t& n) {
+    if (x->ndim == 0) throw value_error("x must have at least one dimension");
+    n = x->shape[x->ndim - 1];
+    if (n > kMaxCols) {
+        throw value_error("the hidden size of x is " + std::to_string(n) + ", at most " +
+                          std::to_string(kMaxCols) + " is supported");
+    }
+    rows = 1;
+    for (int i = 0; i + 1 < x->ndim; ++i) rows *= x->shape[i];
+    if (rows > kMaxGridX) {
+        throw value_error("x has " + std::to_string(rows) + " rows, at most " +
+                          std::to_string(kMaxGridX) + " are supported");
+    }
+}
+
+void check_like(const kcr_tensor* t, const kcr_tensor* like, const char* name,
+                const char* like_name) {
+    if (shape_of(*t) != shape_of(*like) || t->dtype != like->dtype) {
+        throw value_error(std::string(name) + " must have the shape and dtype of " + like_name);
+    }
+}
+
+void check_f32(const kcr_tensor* t, int64_t count, const char* name) {
+    if (t->dtype != KCR_FLOAT32 || numel(*t) != count) {
+        throw value_error(std::string(name) + " must be a float32 tensor with " +
+                          std::to_string(count) + " elements");
+    }
+}
+
+void check_weight(const kcr_tensor* w, int64_t n) {
+    if (w && (w->ndim != 1 || w->shape[0] != n)) {
+        throw value_error("weight must have shape [" + std::to_string(n) + "], got " +
+                          shape_string(*w));
+    }
+}
+
+void check_input_dtype(const kcr_tensor* x) {
+    if (x->dtype != KCR_FLOAT16 && x->dtype != KCR_BFLOAT16 && x->dtype != KCR_FLOAT32) {
+        throw value_error("unsupported dtype, expected float16, bfloat16 or float32");
+    }
+}
+
+void check_weight_dtype(const kcr_tensor* w, const kcr_tensor* x) {
+    if (w && w->dtype != x->dtype && w->dtype != KCR_FLOAT32) {
+        throw value_error("weight must have the dtype of x or be float32");
+    }
+}
+
+void check_contiguous(const kcr_tensor* t, const char* name) {
+    if (t && !is_contiguous(*t)) throw value_error(std::string(name) + " must be contiguous");
+    require_device(t, name);
+}
+
+// Threads per block for rows of n elements (warp counts of ops.rs:98-106,
+// expressed in 64-lane waves).
+unsigned block_threads(int64_t n) {
+    if (n < 2048) return 128;
+    if (n < 8192) return 256;
+    if (n < 32768) return 512;
+    return 1024;
+}
+
+struct Fwd {
+    const kcr_tensor *y, *rstd, *x, *w;
+    int64_t rows, n;
+    float eps, offset;
+    hipStream_t stream;
+};
+
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
+void launch_wave(const Fwd& f, uint32_t nvec) {
+    const uint64_t waves_needed = static_cast<uint64_t>(f.rows);
+    uint64_t blocks = (waves_needed + kWaves - 1) / kWaves;
+    // One wave per row (the kernel loops if the grid is capped).
+    const uint64_t cap = 2147483647ull;
+    if (blocks > cap) blocks = cap;
+    rms_fwd_wave<X, W, M, AFFINE, CHUNKS><<<static_cast<unsigned>(blocks), 64 * kWaves, 0, f.stream>>>(
+        static_cast<u32x4*>(f.y->data), static_cast<float*>(f.rstd->data),
+        static_cast<const u32x4*>(f.x->data),
+        static_cast<const u32x4*>(AFFINE ? f.w->data : f.x->data), static_cast<uint32_t>(f.rows),
+        nvec, 1.0f / static_cast<float>(f.n), f.eps, f.offset);
+}
+
+template <typename X, typename W, int M, bool AFFINE>
+void launch_fwd(const Fwd& f) {
+    constexpr int VEC = vec_of<X>();
+    const bool aligned = aligned16(f.x->data) && aligned16(f.y->data) &&
+                         (!AFFINE || aligned16(f.w->data));
+    if (aligned && f.n % VEC == 0) {
+        const uint32_t nvec = static_cast<uint32_t>(f.n / VEC);
+        const uint32_t chunks = (nvec + 63) / 64;
+        if (chunks <= 1) return launch_wave<X, W, M, AFFINE, 1>(f, nvec);
+        if (chunks <= 2) return launch_wave<X, W, M, AFFINE, 2>(f, nvec);
+        if (chunks <= 4) return launch_wave<X, W, M, AFFINE, 4>(f, nvec);
+        if (chunks <= 8) return launch_wave<X, W, M, AFFINE, 8>(f, nvec);
+        if (chunks <= 16) return launch_wave<X, W, M, AFFINE, 16>(f, nvec);
+    }
+    rms_fwd_block<X, W, M, AFFINE><<<static_cast<unsigned>(f.rows), block_threads(f.n), 0, f.stream>>>(
+        static_cast<X*>(f.y->data), static_cast<float*>(f.rstd->data),
+        static_cast<const X*>(f.x->data), static_cast<const W*>(AFFINE ? f.w->data : f.x->data),
+        static_cast<uint32_t>(f.n), 1.0f / static_cast<float>(f.n), f.eps, f.offset);
+}
+
+// Dispatch over (mode, X, W, AFFINE) like ops.rs:136-184; `L` is a functor
+// template invoked as L::template run<X, W, M, AFFINE>(args).
+template <template <typename, typename, int, bool> class L, typename Args>
+void dispatch(int mode, const kcr_tensor* x, const kcr_tensor* w, const Args& a) {
+    auto with_mode = [&](auto xtag) {
+        using X = decltype(xtag);
+        auto go = [&](auto wtag, auto affine) {
+            using W = decltype(wtag);
+            constexpr bool AFF = decltype(affine)::value;
+            switch (mode) {
+                case MODE_LLAMA: L<X, W, MODE_LLAMA, AFF>::run(a); break;
+                case MODE_GEMMA: L<X, W, MODE_GEMMA, AFF>::run(a); break;
+                default: L<X, W, MODE_NONE, AFF>::run(a); break;
+            }
+        };
+        if (!w) {
+            go(X{}, std::false_type{});
+        } else if (w->dtype == x->dtype) {
+            go(X{}, std::true_type{});
+        } else {
+            go(float{}, std::true_type{});
+        }
+    };
+    switch (x->dtype) {
+        case KCR_FLOAT16: with_mode(f16_t{}); break;
+        case KCR_BFLOAT16: with_mode(bf16_t{}); break;
+        default: with_mode(float{}); break;
+    }
+}
+
+template <typename X, typename W, int M, bool AFFINE>
+struct FwdLaunch {
+    static void run(const Fwd& f) {
+        launch_fwd<X, W, M, AFFINE>(f);
+        check_launch("launch rms_norm_fwd");
+    }
+};
+
+struct Bwd {
+    const kcr_tensor *dx, *dw_partial, *dy, *x, *w, *rstd;
+    int64_t blocks, rows, n;
+    float offset;
+    hipStream_t stream;
+};
+
+template <typename X, typename W, int M, bool AFFINE>
+struct BwdLaunch {
+    static void run(const Bwd& b) {
+        // Without dy the gradient is read from dx (in place).
+        const void* dy = b.dy ? b.dy->data : b.dx->data;
+        float* dwp = AFFINE ? static_cast<float*>(b.dw_partial->data) : nullptr;
+        rms_bwd_block<X, W, M, AFFINE><<<static_cast<unsigned>(b.blocks), block_threads(b.n), 0, b.stream>>>(
+            static_cast<X*>(b.dx->data), dwp, static_cast<const X*>(dy),
+            static_cast<const X*>(b.x->data), static_cast<const W*>(AFFINE ? b.w->data : b.x->data),
+            static_cast<const float*>(b.rstd->data), static_cast<uint32_t>(b.rows),
+            static_cast<uint32_t>(b.n), 1.0f / static_cast<float>(b.n), b.offset);
+        check_launch("launch rms_norm_bwd");
+    }
+};
+
+}  // namespace
+}  // namespace kcr
+
+using namespace kcr;
+
+extern "C" int kcr_rms_norm_forward(const kcr_tensor* y, const kcr_tensor* rstd,
+                                    const kcr_tensor* x, const kcr_tensor* weight, double eps,
+                                    double offset, const char* casting_mode, void* stream) {
+    return guarded([&] {
+        if (!y || !rstd || !x) throw value_error("y, rstd and x are required");
+        const int mode = parse_mode(casting_mode);
+        int64_t rows, n;
+        rows_and_cols(x, rows, n);
+        check_like(y, x, "y", "x");
+        check_f32(rstd, rows, "rstd");
+        check_weight(weight, n);
+        if (rows == 0 || n == 0) return;
+        check_input_dtype(x);
+        check_weight_dtype(weight, x);
+        check_contiguous(x, "x");
+        check_contiguous(y, "y");
+        check_contiguous(rstd, "rstd");
+        check_contiguous(weight, "weight");
+        Fwd f{y, rstd, x, weight, rows, n, static_cast<float>(eps), static_cast<float>(offset),
+              static_cast<hipStream_t>(stream)};
+        dispatch<FwdLaunch>(mode, x, weight, f);
+    });
+}
+
+extern "C" int kcr_rms_norm_backward(const kcr_tensor* dx, const kcr_tensor* dw_partial,
+                                     const kcr_tensor* dy, const kcr_tensor* x,
+                                     const kcr_tensor* weight, const kcr_tensor* rstd,
+                                     double offset, const char* casting_mode, void* stream) {
+    return guarded([&] {
+        if (!dx || !x || !rstd) throw value_error("dx, x and rstd are required");
+        const int mode = parse_mode(casting_mode);
+        int64_t rows, n;
+        rows_and_cols(x, rows, n);
+        check_like(dx, x, "dx", "x");
+        if (dy) check_like(dy, x, "dy", "x");
+        check_f32(rstd, rows, "rstd");
+        check_weight(weight, n);
+        if (n == 0) return;
+        int64_t blocks;
+        if (weight && dw_partial) {
+            if (dw_partial->ndim != 2 || dw_partial->shape[1] != n || dw_partial->shape[0] < 1 ||
+                dw_partial->shape[0] > kMaxGridX) {
+                throw value_error("dw_partial must have shape [blocks, " + std::to_string(n) +
+                                  "] with blocks > 0, got " + shape_string(*dw_partial));
+            }
+            blocks = dw_partial->shape[0];
+            check_f32(dw_partial, blocks * n, "dw_partial");
+        } else if (weight) {
+            throw value_error("dw_partial is required with a weight");
+        } else {
+            if (rows == 0) return;
+            blocks = rows;
+        }
+        check_input_dtype(x);
+        check_weight_dtype(weight, x);
+        check_contiguous(x, "x");
+        check_contiguous(dx, "dx");
+        check_contiguous(dy, "dy");
+        check_contiguous(rstd, "rstd");
+        check_contiguous(weight, "weight");
+        if (weight) check_contiguous(dw_partial, "dw_partial");
+        Bwd b{dx, weight ? dw_partial : nullptr, dy, x, weight, rstd, blocks, rows, n,
+              static_cast<float>(offset), static_cast<hipStream_t>(stream)};
+        dispatch<BwdLaunch>(mode, x, weight, b);
+    });
+}
+
+extern "C" int kcr_rms_norm_reduce_weight_grad(const kcr_tensor* dw, const kcr_tensor* dw_partial,
+                                               void* stream) {
+    return guarded([&] {
+        if (!dw || !dw_partial) throw value_error("dw and dw_partial are required");
+        if (dw->ndim != 1) {
+            throw value_error("dw must be one-dimensional, got shape " + shape_string(*dw));
+        }
+        const int64_t n = dw->shape[0];
+        if (dw_partial->ndim != 2 || dw_partial->shape[1] != n ||
+            dw_partial->shape[0] > 4294967295ll) {
+            throw value_error("dw_partial must have shape [blocks, " + std::to_string(n) +
+                              "], got " + shape_string(*dw_partial));
+        }
+        const int64_t blocks = dw_partial->shape[0];
+        check_f32(dw_partial, blocks * n, "dw_partial");
+        if (n == 0) return;
+        check_contiguous(dw, "dw");
+        check_contiguous(dw_partial, "dw_partial");
+        auto s = static_cast<hipStream_t>(stream);
+        const unsigned grid = static_cast<unsigned>((n + 255) / 256);
+        const auto* p = static_cast<const float*>(dw_partial->data);
+        switch (dw->dtype) {
+            case KCR_FLOAT16:
+                reduce_weight_grad<f16_t><<<grid, 256, 0, s>>>(static_cast<f16_t*>(dw->data), p,
+                                                               blocks, n);
+                break;
+            case KCR_BFLOAT16:
+                reduce_weight_grad<bf16_t><<<grid, 256, 0, s>>>(static_cast<bf16_t*>(dw->data), p,
+                                                                blocks, n);
+                break;
+            case KCR_FLOAT32:
+                reduce_weight_grad<float><<<grid, 256, 0, s>>>(static_cast<float*>(dw->data), p,
+                                                               blocks, n);
+                break;
+            default:
+                throw value_error("unsupported dtype for dw, expected float16, bfloat16 or float32");
+        }
+        check_launch("launch reduce_weight_grad");
+    });
+}

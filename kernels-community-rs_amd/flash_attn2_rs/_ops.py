@@ -1,0 +1,211 @@
+"""`ops` of flash-attn2-rs: the tvm-ffi exports on the hot path, with the reference's
+positional signatures and return conventions, backed by libkcr_hip.so.
+
+  fwd(q, k, v, alibi, scale, causal, wl, wr, softcap[, p, seed, offset][, out])
+      -> [out, lse]                          host/forward/mod.rs:52-61, 815-833
+  fwd_lse(..., out) -> lse                   host/forward/mod.rs:835-853
+  varlen_fwd_explicit(q, k, v, cuq, cuk, seqused_k, leftpad_k, alibi, scale, causal,
+      left, right, softcap, p, state, max_q, max_k, return_softmax, zero_tensors)
+      -> [out, lse, probabilities]           host/varlen/mod.rs:21-670
+  bwd_preprocess(dout, out, p) -> delta      host/backward.rs:628-737
+  bwd_dq / bwd_dkv / bwd_all(q, k, v, dout, lse, delta, alibi, scale, causal, left,
+      right, softcap, p, rng_state) -> dq | [dk, dv] | [dq, dk, dv]
+                                             host/backward.rs:14-626
+  varlen_bwd_explicit(q, k, v, dout, out, lse, cuq, cuk, alibi, scale, causal, left,
+      right, softcap, p, state, max_q, max_k, zero_tensors) -> [dq, dk, dv, delta]
+                                             host/varlen/backward.rs:15-546
+
+Outputs the reference allocates with `TVMFFIEnvTensorAlloc` are allocated here with
+torch's allocator (the same allocator tvm-ffi forwards to under torch). Inputs
+whose rows are not 16-byte aligned are repacked first, as the reference does
+with `copy_attention_layout` (host/layout.rs:46-125). Dropout (p > 0) is not part
+of this build.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from types import SimpleNamespace
+
+import torch
+
+from kcr_native import call, describe, lib, op_namespace_prefixer, ref, stream_of
+
+torch_add_op_namespace_prefix = op_namespace_prefixer("flash_attn2")
+
+
+def _rows_aligned(t: torch.Tensor) -> bool:
+    if t.data_ptr() % 16:
+        return False
+    return all(s % 8 == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+
+
+def _packed(t):
+    """A 16-byte aligned view of `t` with unit last stride (repacked if needed)."""
+    if t is None or t.numel() == 0:
+        return t
+    if t.stride(-1) == 1 and _rows_aligned(t):
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
+def _no_dropout(p):
+    p = float(p)
+    if not (p == p) or not 0.0 <= p < 1.0:
+        raise ValueError("p_dropout must be finite and in [0, 1) as float32")
+    if p > 0.0:
+        raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
+
+
+def _scale_args(scale):
+    return (0, ctypes.c_double(0.0)) if scale is None else (1, ctypes.c_double(float(scale)))
+
+
+def _fwd_impl(args, lse_only):
+    n = len(args)
+    if n not in (9, 10, 12, 13):
+        raise ValueError(
+            "fwd expects 9 positional arguments (q, k, v, alibi_slopes, softmax_scale, "
+            "is_causal, window_size_left, window_size_right, softcap), optionally followed by "
+            f"p_dropout, seed, offset, and/or an output tensor; got {n}"
+        )
+    q, k, v, alibi, scale, causal, wl, wr, softcap = args[:9]
+    if n >= 12:
+        _no_dropout(args[9])
+    supplied = args[-1] if n in (10, 13) else None
+    if lse_only and supplied is None:
+        raise ValueError("LSE-only forward requires a supplied output")
+    if q.ndim != 4:
+        raise ValueError(f"q must have 4 dimensions [B, S, H, D], got shape {list(q.shape)}")
+    b, sq, h, d = q.shape
+    qp, kp, vp = _packed(q), _packed(k), _packed(v)
+    copy_out = supplied is not None and (
+        supplied.stride(-1) != 1 or not _rows_aligned(supplied)
+        or any(supplied.data_ptr() == t.data_ptr() for t in (q, k, v))
+    )
+    out = supplied if supplied is not None and not copy_out else torch.empty(
+        q.shape, dtype=q.dtype, device=q.device)
+    if supplied is not None and (supplied.shape != q.shape or supplied.dtype != q.dtype):
+        raise ValueError("out must match q's shape, dtype and device")
+    lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
+    has_scale, sc = _scale_args(scale)
+    descs = [describe(t) for t in (qp, kp, vp, alibi)]
+    call("kcr_flash_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
+         ctypes.c_int64(int(wl)), ctypes.c_int64(int(wr)), ctypes.c_double(float(softcap)),
+         ref(describe(out)), ref(describe(lse)), stream_of(q))
+    if copy_out:
+        supplied.copy_(out)
+        out = supplied
+    return lse if lse_only else [out, lse]
+
+
+def fwd(*args):
+    return _fwd_impl(args, False)
+
+
+def fwd_lse(*args):
+    return _fwd_impl(args, True)
+
+
+def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi, scale,
+                        causal, left, right, softcap, p, state, max_q, max_k, return_softmax,
+                        zero_tensors, block_table=None):
+    if block_table is not None:
+        raise NotImplementedError("paged K/V (block_table) is not supported by this build")
+    _no_dropout(p)
+    if return_softmax:
+        raise ValueError("return_softmax requires nonzero dropout and a CUDA RNG-state tensor")
+    qp, kp, vp = _packed(q), _packed(k), _packed(v)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
+    has_scale, sc = _scale_args(scale)
+    descs = [describe(t) for t in (qp, kp, vp, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi)]
+    call("kcr_flash_varlen_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
+         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)),
+         ctypes.c_int64(int(max_q)), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)),
+         ref(describe(out)), ref(describe(lse)), stream_of(q))
+    probabilities = torch.empty(0, dtype=q.dtype, device=q.device)
+    return [out, lse, probabilities]
+
+
+def bwd_preprocess(dout, out, p):
+    _no_dropout(p)
+    if out.ndim != 4 or dout.shape != out.shape:
+        raise ValueError("dout and out must share shape, dtype and device")
+    b, s, h, d = out.shape
+    rounded = (s + 127) // 128 * 128
+    delta = torch.empty((b, h, rounded), dtype=torch.float32, device=out.device)
+    call("kcr_flash_bwd_preprocess", ref(describe(_packed(dout))), ref(describe(_packed(out))),
+         ctypes.c_double(float(p)), ref(describe(delta)), stream_of(out))
+    return delta
+
+
+def _bwd(args, want_q, want_kv):
+    if len(args) != 14:
+        raise ValueError(
+            "backward component expects q, k, v, dout, lse, delta, alibi, scale, causal, left, "
+            "right, softcap, dropout, rng_state"
+        )
+    q, k, v, dout, lse, delta, alibi, scale, causal, left, right, softcap, p, _state = args
+    _no_dropout(p)
+    qp, kp, vp, dp = _packed(q), _packed(k), _packed(v), _packed(dout)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device) if want_q else None
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device) if want_kv else None
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device) if want_kv else None
+    b, sq, h, d = q.shape
+    ws_bytes = lib.kcr_flash_bwd_workspace_bytes(b, h, sq, d)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    has_scale, sc = _scale_args(scale)
+    descs = [describe(t) for t in (qp, kp, vp, dp, lse, delta, alibi)]
+    call("kcr_flash_bwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
+         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)),
+         ref(describe(dq)), ref(describe(dk)), ref(describe(dv)),
+         ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), stream_of(q))
+    return dq, dk, dv
+
+
+def bwd_dq(*args):
+    return _bwd(args, True, False)[0]
+
+
+def bwd_dkv(*args):
+    _, dk, dv = _bwd(args, False, True)
+    return [dk, dv]
+
+
+def bwd_all(*args):
+    return list(_bwd(args, True, True))
+
+
+def varlen_bwd_explicit(q, k, v, dout, out, lse, cu_seqlens_q, cu_seqlens_k, alibi, scale, causal,
+                        left, right, softcap, p, state, max_q, max_k, zero_tensors):
+    _no_dropout(p)
+    qp, kp, vp, dp, op = (_packed(t) for t in (q, k, v, dout, out))
+    batch = cu_seqlens_q.numel() - 1
+    tq, h, d = q.shape
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty((h, tq + 128 * batch), dtype=torch.float32, device=q.device)
+    ws_bytes = lib.kcr_flash_varlen_bwd_workspace_bytes(tq, h, batch, d)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    has_scale, sc = _scale_args(scale)
+    descs = [describe(t) for t in (qp, kp, vp, dp, op, lse, cu_seqlens_q, cu_seqlens_k, alibi)]
+    call("kcr_flash_varlen_bwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
+         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)),
+         ctypes.c_int64(int(max_q)), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)),
+         ref(describe(dq)), ref(describe(dk)), ref(describe(dv)), ref(describe(delta)),
+         ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), stream_of(q))
+    return [dq, dk, dv, delta]
+
+
+ops = SimpleNamespace(
+    fwd=fwd,
+    fwd_lse=fwd_lse,
+    varlen_fwd_explicit=varlen_fwd_explicit,
+    bwd_preprocess=bwd_preprocess,
+    bwd_dq=bwd_dq,
+    bwd_dkv=bwd_dkv,
+    bwd_all=bwd_all,
+    varlen_bwd_explicit=varlen_bwd_explicit,
+)

@@ -1,0 +1,194 @@
+"""Torch custom ops and autograd Functions behind flash_attn_func /
+flash_attn_varlen_func, mirroring flash-attn2-rs/tvm-ffi-ext/flash_attn2_rs/
+_torch_interface.py:19-555: head sizes that are not a multiple of 8 are
+zero-padded, QKV / KV packings are unbound, and the native forward / backward run
+as opaque custom ops with fake (meta) implementations for torch.compile."""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from ._ops import torch_add_op_namespace_prefix as add_op_namespace_prefix
+from .flash_attn_interface import bwd, fwd, varlen_bwd, varlen_fwd
+
+
+def _custom_op(name):
+    return torch.library.custom_op(add_op_namespace_prefix(name), mutates_args=(), device_types="cuda")
+
+
+@_custom_op("_dense_forward")
+def _dense_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
+                   left: int, right: int, softcap: float,
+                   slopes: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    out, lse, _, _ = fwd(q, k, v, alibi_slopes=slopes, softmax_scale=scale, is_causal=causal,
+                         window_size_left=left, window_size_right=right, softcap=softcap)
+    return out, lse
+
+
+@_dense_forward.register_fake
+def _(q, k, v, scale, causal, left, right, softcap, slopes):
+    b, sq, h, _ = q.shape
+    return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
+
+
+@_custom_op("_dense_backward")
+def _dense_backward(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    out: torch.Tensor, lse: torch.Tensor, scale: float, causal: bool, left: int,
+                    right: int, softcap: float, slopes: Optional[torch.Tensor],
+                    deterministic: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dq, dk, dv, _ = bwd(dout, q, k, v, out, lse, alibi_slopes=slopes, softmax_scale=scale,
+                        is_causal=causal, window_size_left=left, window_size_right=right,
+                        softcap=softcap, deterministic=deterministic)
+    return dq, dk, dv
+
+
+@_dense_backward.register_fake
+def _(dout, q, k, v, out, lse, scale, causal, left, right, softcap, slopes, deterministic):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _pad(dim, *tensors):
+    if dim % 8:
+        return tuple(torch.nn.functional.pad(x, (0, 8 - dim % 8)) for x in tensors)
+    return tuple(x.contiguous() if x.stride(-1) != 1 else x for x in tensors)
+
+
+class _DenseAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
+                alibi_slopes, deterministic, return_attn_probs, packing):
+        if packing == 3:
+            if q.ndim != 5 or q.shape[2] != 3:
+                raise ValueError("qkv must have shape [B, S, 3, H, D]")
+            q, k, v = q.unbind(2)
+        elif packing == 2:
+            if k.ndim != 5 or k.shape[2] != 2:
+                raise ValueError("kv must have shape [B, Sk, 2, Hk, D]")
+            k, v = k.unbind(2)
+        if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+            raise ValueError("q, k, v must have shape [B, S, H, D]")
+        if dropout_p:
+            raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
+        dim = q.shape[-1]
+        if not 0 < dim <= 256:
+            raise ValueError("head size must be in 1..256")
+        scale = dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+        q, k, v = _pad(dim, q, k, v)
+        left, right = window_size
+        out, lse = _dense_forward(q, k, v, scale, bool(causal), int(left), int(right),
+                                  float(softcap), alibi_slopes)
+        ctx.save_for_backward(q, k, v, out, lse, alibi_slopes)
+        ctx.options = (scale, bool(causal), int(left), int(right), float(softcap), bool(deterministic))
+        ctx.dim, ctx.packing = dim, packing
+        out = out[..., :dim]
+        if return_attn_probs:
+            return out, lse, torch.empty(0, device=q.device, dtype=q.dtype)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dout, *unused):
+        q, k, v, out, lse, slopes = ctx.saved_tensors
+        scale, causal, left, right, cap, deterministic = ctx.options
+        (dout,) = _pad(ctx.dim, dout)
+        dq, dk, dv = _dense_backward(dout, q, k, v, out, lse, scale, causal, left, right, cap,
+                                     slopes, deterministic)
+        dq, dk, dv = (x[..., : ctx.dim] for x in (dq, dk, dv))
+        if ctx.packing == 3:
+            grads = (torch.stack((dq, dk, dv), dim=2), None, None)
+        elif ctx.packing == 2:
+            grads = (dq, torch.stack((dk, dv), dim=2), None)
+        else:
+            grads = (dq, dk, dv)
+        return (*grads, *(None,) * 9)
+
+
+@_custom_op("_varlen_forward")
+def _varlen_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cuq: torch.Tensor,
+                    cuk: torch.Tensor, max_q: int, max_k: int, scale: float, causal: bool,
+                    left: int, right: int, softcap: float,
+                    slopes: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    out, lse, _, _ = varlen_fwd(q, k, v, cuq, cuk, max_seqlen_q=max_q, max_seqlen_k=max_k,
+                                softmax_scale=scale, is_causal=causal, window_size_left=left,
+                                window_size_right=right, softcap=softcap, alibi_slopes=slopes)
+    return out, lse
+
+
+@_varlen_forward.register_fake
+def _(q, k, v, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes):
+    total, h, _ = q.shape
+    return torch.empty_like(q), q.new_empty((h, total), dtype=torch.float32)
+
+
+@_custom_op("_varlen_backward")
+def _varlen_backward(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     out: torch.Tensor, lse: torch.Tensor, cuq: torch.Tensor, cuk: torch.Tensor,
+                     max_q: int, max_k: int, scale: float, causal: bool, left: int, right: int,
+                     softcap: float, slopes: Optional[torch.Tensor]
+                     ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dq, dk, dv, _ = varlen_bwd(dout, q, k, v, out, lse, cuq, cuk, alibi_slopes=slopes,
+                               max_seqlen_q=max_q, max_seqlen_k=max_k, softmax_scale=scale,
+                               is_causal=causal, window_size_left=left, window_size_right=right,
+                               softcap=softcap)
+    return dq, dk, dv
+
+
+@_varlen_backward.register_fake
+def _(dout, q, k, v, out, lse, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+class _VarlenAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cuq, cuk, max_q, max_k, dropout_p, softmax_scale, causal,
+                window_size, softcap, slopes, deterministic, return_probs, block_table, packing):
+        if block_table is not None:
+            raise NotImplementedError("paged K/V (block_table) is not supported by this build")
+        if cuk is None:
+            cuk = cuq
+        if packing == 3:
+            if q.ndim != 4 or q.shape[1] != 3:
+                raise ValueError("qkv must have shape [total, 3, H, D]")
+            q, k, v = q.unbind(1)
+        elif packing == 2:
+            if k.ndim != 4 or k.shape[1] != 2:
+                raise ValueError("kv must have shape [total_k, 2, Hk, D]")
+            k, v = k.unbind(1)
+        if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+            raise ValueError("q must be rank 3; k/v must be rank 4 with block_table, otherwise rank 3")
+        if dropout_p:
+            raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
+        dim = q.shape[-1]
+        if not 0 < dim <= 256:
+            raise ValueError("head size must be in 1..256")
+        scale = dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+        q, k, v = _pad(dim, q, k, v)
+        left, right = window_size
+        out, lse = _varlen_forward(q, k, v, cuq, cuk, int(max_q), int(max_k), scale, bool(causal),
+                                   int(left), int(right), float(softcap), slopes)
+        ctx.save_for_backward(q, k, v, out, lse, cuq, cuk, slopes)
+        ctx.options = (int(max_q), int(max_k), scale, bool(causal), int(left), int(right), float(softcap))
+        ctx.dim, ctx.packing = dim, packing
+        out = out[..., :dim]
+        if return_probs:
+            return out, lse, torch.empty(0, device=q.device, dtype=q.dtype)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dout, *unused):
+        q, k, v, out, lse, cuq, cuk, slopes = ctx.saved_tensors
+        max_q, max_k, scale, causal, left, right, cap = ctx.options
+        (dout,) = _pad(ctx.dim, dout)
+        dq, dk, dv = _varlen_backward(dout, q, k, v, out, lse, cuq, cuk, max_q, max_k, scale,
+                                      causal, left, right, cap, slopes)
+        dq, dk, dv = (x[..., : ctx.dim] for x in (dq, dk, dv))
+        if ctx.packing == 3:
+            grads = (torch.stack((dq, dk, dv), dim=1), None, None)
+        elif ctx.packing == 2:
+            grads = (dq, torch.stack((dk, dv), dim=1), None)
+        else:
+            grads = (dq, dk, dv)
+        return (*grads, *(None,) * 14)

@@ -1,0 +1,286 @@
+"""FlashAttention-2 v2-style Python API on MI355X, mirroring
+flash-attn2-rs/tvm-ffi-ext/flash_attn2_rs/flash_attn_interface.py:
+
+  fwd / bwd / varlen_fwd / varlen_bwd          (interface.py:732-1471)
+  flash_attn_func, flash_attn_qkvpacked_func, flash_attn_kvpacked_func,
+  flash_attn_varlen_func, flash_attn_varlen_qkvpacked_func,
+  flash_attn_varlen_kvpacked_func              (interface.py:1707-1903)
+
+Same argument names, defaults, return lists and error kinds for the validation
+that matters on this path (dtype, device, shapes, head size, GQA divisibility).
+Dropout, paged K/V and the KV-cache entry points are outside this build and
+raise NotImplementedError.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ._ops import ops
+
+
+def _cpu_dispatch(op):
+    raise NotImplementedError(f"flash_attn2_rs::{op} has no CPU implementation")
+
+
+def _check_dropout(p):
+    p = float(p)
+    if not math.isfinite(p) or not 0.0 <= p < 1.0:
+        raise RuntimeError("p_dropout must be finite and in [0, 1) as float32")
+    if p > 0.0:
+        raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
+    return p
+
+
+def _validate(q, k, v, out, alibi, softcap, *, packed=False):
+    rank = 3 if packed else 4
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or t.ndim != rank:
+            raise RuntimeError(f"{name} must be a CUDA tensor of shape [B, S, H, D]")
+        if t.dtype not in (torch.float16, torch.bfloat16) or t.dtype != q.dtype:
+            raise RuntimeError(
+                "FlashAttention only support fp16 and bf16 data type"
+                if name == "q"
+                else f"query and {'key' if name == 'k' else 'value'} must have the same dtype"
+            )
+        if t.device != q.device:
+            raise RuntimeError("q, k, v must share device")
+        if t.stride(-1) != 1:
+            raise RuntimeError("Input tensor must have contiguous last dimension")
+    if packed:
+        b = 1
+        h, d = q.shape[-2:]
+    else:
+        b, _, h, d = q.shape
+    if not 0 < b <= 65535 or not 0 < h <= 65535 or d < 8 or d > 256 or d % 8:
+        raise RuntimeError(
+            "batch and heads must each be in 1..65535 and head size a multiple of 8 in 8..256"
+        )
+    if (not packed and k.shape[0] != b) or k.shape[-1] != d or k.shape != v.shape:
+        raise RuntimeError("k and v must have matching [B, Sk, Hk, D] shapes")
+    if k.shape[-2] == 0 or h % k.shape[-2]:
+        raise RuntimeError("the number of KV heads must divide the number of query heads")
+    if out is not None:
+        if (not isinstance(out, torch.Tensor) or out.device != q.device or out.dtype != q.dtype
+                or out.shape != q.shape):
+            raise RuntimeError("out must match q's shape, dtype and device")
+        if out.stride(-1) != 1:
+            raise RuntimeError("out must have unit last stride")
+    if alibi is not None:
+        if not isinstance(alibi, torch.Tensor) or alibi.device != q.device or alibi.dtype != torch.float32:
+            raise RuntimeError("alibi_slopes must be float32 on q's device")
+
+
+def fwd(q, k, v, out=None, alibi_slopes=None, p_dropout=0.0, softmax_scale=None, is_causal=False,
+        window_size_left=-1, window_size_right=-1, softcap=0.0, return_softmax=False, gen=None):
+    """Return [output, LSE, probabilities, RNG state] (interface.py:732-852)."""
+    if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
+        _cpu_dispatch("fwd")
+    p = _check_dropout(p_dropout)
+    if return_softmax and p == 0:
+        raise RuntimeError("return_softmax is only supported when p_dropout > 0.0")
+    _validate(q, k, v, out, alibi_slopes, softcap)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
+    if q.shape[1] == 1 and alibi_slopes is None:
+        is_causal = False  # v2's single-query convention
+    if alibi_slopes is not None:
+        alibi_slopes = alibi_slopes.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    lse = ops.fwd_lse(q, k, v, alibi_slopes, float(softmax_scale), bool(is_causal),
+                      int(window_size_left), int(window_size_right), float(softcap), out)
+    probabilities = torch.empty(0, device=q.device, dtype=q.dtype)
+    state = torch.empty(2, device=q.device, dtype=torch.int64)
+    return [out, lse, probabilities, state]
+
+
+def fwd_explicit(*args):
+    return ops.fwd(*args)
+
+
+def _finish_gradients(actuals, supplied, sources):
+    grads = []
+    for actual, buf, source in zip(actuals, supplied, sources):
+        if buf is None:
+            grads.append(actual)
+        else:
+            with torch.no_grad():
+                buf.copy_(actual)
+            grads.append(buf)
+    return grads
+
+
+def bwd(dout, q, k, v, out, softmax_lse, dq=None, dk=None, dv=None, alibi_slopes=None,
+        p_dropout=0.0, softmax_scale=None, is_causal=False, window_size_left=-1,
+        window_size_right=-1, softcap=0.0, deterministic=False, gen=None, rng_state=None):
+    """Return [dQ, dK, dV, softmax_d] (interface.py:855-1009). Both the
+    deterministic and default paths are deterministic here (fixed-order GQA sums)."""
+    if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
+        _cpu_dispatch("bwd")
+    p = _check_dropout(p_dropout)
+    _validate(q, k, v, None, alibi_slopes, softcap)
+    for name, t in (("dout", dout), ("out", out)):
+        if not isinstance(t, torch.Tensor) or t.shape != q.shape or t.device != q.device or t.dtype != q.dtype:
+            raise RuntimeError(f"{name} must match q's shape, dtype and device")
+    if (not isinstance(softmax_lse, torch.Tensor) or softmax_lse.shape != (q.shape[0], q.shape[2], q.shape[1])
+            or softmax_lse.dtype != torch.float32 or not softmax_lse.is_contiguous()):
+        raise RuntimeError("softmax_lse must be contiguous float32 [B, H, Sq] on q's device")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
+    if alibi_slopes is not None:
+        alibi_slopes = alibi_slopes.contiguous()
+    delta = ops.bwd_preprocess(dout, out, p)
+    args = (q, k, v, dout, softmax_lse, delta, alibi_slopes, float(softmax_scale), bool(is_causal),
+            int(window_size_left), int(window_size_right), float(softcap), p, None)
+    if deterministic:
+        grad_q = ops.bwd_dq(*args)
+        grad_k, grad_v = ops.bwd_dkv(*args)
+    else:
+        grad_q, grad_k, grad_v = ops.bwd_all(*args)
+    return [*_finish_gradients((grad_q, grad_k, grad_v), (dq, dk, dv), (q, k, v)), delta]
+
+
+def _check_varlen_meta(q, cu_seqlens_q, cu_seqlens_k):
+    if not isinstance(cu_seqlens_q, torch.Tensor) or cu_seqlens_q.ndim != 1 or cu_seqlens_q.numel() < 2:
+        raise RuntimeError("cu_seqlens_q must have shape [batch + 1]")
+    batch = cu_seqlens_q.numel() - 1
+    if batch > 65535:
+        raise RuntimeError("batch must not exceed 65535")
+    for name, t in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
+        if (not isinstance(t, torch.Tensor) or t.shape != (batch + 1,) or t.dtype != torch.int32
+                or t.device != q.device or not t.is_contiguous()):
+            raise RuntimeError(f"{name} must be contiguous int32 ({batch + 1},) on q's device")
+    return batch
+
+
+def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, leftpad_k=None,
+               block_table=None, alibi_slopes=None, max_seqlen_q=0, max_seqlen_k=0, p_dropout=0.0,
+               softmax_scale=None, zero_tensors=False, is_causal=False, window_size_left=-1,
+               window_size_right=-1, softcap=0.0, return_softmax=False, gen=None):
+    """Packed forward, returning [out, LSE, probabilities, RNG state] (interface.py:1012-1241)."""
+    if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
+        _cpu_dispatch("varlen_fwd")
+    if block_table is not None:
+        raise NotImplementedError("paged K/V (block_table) is not supported by this build")
+    p = _check_dropout(p_dropout)
+    if return_softmax and p == 0:
+        raise RuntimeError("return_softmax is only supported when p_dropout > 0.0")
+    _validate(q, k, v, out, alibi_slopes, softcap, packed=True)
+    _check_varlen_meta(q, cu_seqlens_q, cu_seqlens_k)
+    if not 0 <= int(max_seqlen_q) <= 2**31 - 128 or not 0 <= int(max_seqlen_k) <= 2**31 - 128:
+        raise RuntimeError("maximum sequence lengths must fit nonnegative int32 with rounding")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
+    if alibi_slopes is not None:
+        alibi_slopes = alibi_slopes.contiguous()
+    output, lse, probabilities = ops.varlen_fwd_explicit(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi_slopes,
+        float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),
+        float(softcap), p, None, int(max_seqlen_q), int(max_seqlen_k), bool(return_softmax),
+        bool(zero_tensors))
+    if out is not None:
+        out.copy_(output)
+        output = out
+    state = torch.empty(2, device=q.device, dtype=torch.int64)
+    return [output, lse, probabilities, state]
+
+
+def varlen_bwd(dout, q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, dq=None, dk=None,
+               dv=None, alibi_slopes=None, max_seqlen_q=0, max_seqlen_k=0, p_dropout=0.0,
+               softmax_scale=None, zero_tensors=False, is_causal=False, window_size_left=-1,
+               window_size_right=-1, softcap=0.0, deterministic=False, gen=None, rng_state=None):
+    """Packed backward returning [dQ, dK, dV, softmax_d] (interface.py:1244-1471)."""
+    if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
+        _cpu_dispatch("varlen_bwd")
+    p = _check_dropout(p_dropout)
+    if any(not isinstance(x, torch.Tensor) or x.ndim != 3 for x in (q, k, v)):
+        raise RuntimeError("q, k, v must have shape [total_tokens, heads, head_size]")
+    _validate(q, k, v, None, alibi_slopes, softcap, packed=True)
+    batch = _check_varlen_meta(q, cu_seqlens_q, cu_seqlens_k)
+    h = q.shape[1]
+    for name, t in (("dout", dout), ("out", out)):
+        if (not isinstance(t, torch.Tensor) or t.shape != q.shape or t.device != q.device
+                or t.dtype != q.dtype or t.stride(-1) != 1):
+            raise RuntimeError(f"{name} must match q's shape, dtype and device with unit last stride")
+    if (not isinstance(softmax_lse, torch.Tensor) or softmax_lse.shape != (h, q.shape[0])
+            or softmax_lse.dtype != torch.float32 or not softmax_lse.is_contiguous()):
+        raise RuntimeError("softmax_lse must be contiguous float32 [H,total_q] on q's device")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
+    if alibi_slopes is not None:
+        alibi_slopes = alibi_slopes.contiguous()
+    grad_q, grad_k, grad_v, softmax_d = ops.varlen_bwd_explicit(
+        q, k, v, dout, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, alibi_slopes,
+        float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),
+        float(softcap), p, None, int(max_seqlen_q), int(max_seqlen_k), bool(zero_tensors))
+    return [*_finish_gradients((grad_q, grad_k, grad_v), (dq, dk, dv), (q, k, v)), softmax_d]
+
+
+def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1),
+                    softcap=0.0, alibi_slopes=None, deterministic=False, return_attn_probs=False):
+    """Dense attention with Q/K/V autograd, MQA/GQA and head padding (interface.py:1707)."""
+    from ._torch_interface import _DenseAttention
+
+    return _DenseAttention.apply(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
+                                 alibi_slopes, deterministic, return_attn_probs, 0)
+
+
+def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=False,
+                              window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                              deterministic=False, return_attn_probs=False):
+    """Self-attention with autograd for packed [B, S, 3, H, D] input."""
+    from ._torch_interface import _DenseAttention
+
+    return _DenseAttention.apply(qkv, None, None, dropout_p, softmax_scale, causal, window_size,
+                                 softcap, alibi_slopes, deterministic, return_attn_probs, 3)
+
+
+def flash_attn_kvpacked_func(q, kv, dropout_p=0.0, softmax_scale=None, causal=False,
+                             window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                             deterministic=False, return_attn_probs=False):
+    """Attention with autograd for Q [B, Sq, H, D] and KV [B, Sk, 2, Hk, D]."""
+    from ._torch_interface import _DenseAttention
+
+    return _DenseAttention.apply(q, kv, None, dropout_p, softmax_scale, causal, window_size,
+                                 softcap, alibi_slopes, deterministic, return_attn_probs, 2)
+
+
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                           dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1),
+                           softcap=0.0, alibi_slopes=None, deterministic=False,
+                           return_attn_probs=False, block_table=None):
+    """Variable-length attention with autograd (interface.py:1800)."""
+    from ._torch_interface import _VarlenAttention
+
+    cuk = None if cu_seqlens_k is cu_seqlens_q else cu_seqlens_k
+    return _VarlenAttention.apply(q, k, v, cu_seqlens_q, cuk, max_seqlen_q, max_seqlen_k, dropout_p,
+                                  softmax_scale, causal, window_size, softcap, alibi_slopes,
+                                  deterministic, return_attn_probs, block_table, 0)
+
+
+def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, dropout_p=0.0, softmax_scale=None,
+                                     causal=False, window_size=(-1, -1), softcap=0.0,
+                                     alibi_slopes=None, deterministic=False,
+                                     return_attn_probs=False):
+    """Autograd for variable-length packed [total, 3, H, D] QKV."""
+    from ._torch_interface import _VarlenAttention
+
+    return _VarlenAttention.apply(qkv, None, None, cu_seqlens, None, max_seqlen, max_seqlen,
+                                  dropout_p, softmax_scale, causal, window_size, softcap,
+                                  alibi_slopes, deterministic, return_attn_probs, None, 3)
+
+
+def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                    dropout_p=0.0, softmax_scale=None, causal=False,
+                                    window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                                    deterministic=False, return_attn_probs=False):
+    """Autograd for variable-length Q and packed [total_k, 2, Hk, D] KV."""
+    from ._torch_interface import _VarlenAttention
+
+    cuk = None if cu_seqlens_k is cu_seqlens_q else cu_seqlens_k
+    return _VarlenAttention.apply(q, kv, None, cu_seqlens_q, cuk, max_seqlen_q, max_seqlen_k,
+                                  dropout_p, softmax_scale, causal, window_size, softcap,
+                                  alibi_slopes, deterministic, return_attn_probs, None, 2)

@@ -1,0 +1,166 @@
+"""FlashAttention-2 oracle (numpy) -- test infrastructure only.
+
+Restates the reference tests' fp32 attention, flash-attn2-rs/tests/test_fwd.py:36-85
+(`reference_attention`), with FlashAttention's conventions for rows that see no
+key: output 0 and LSE +inf (tests/test_fwd.py:158-168, host/forward/mod.rs:548-572).
+  scores = q k^T * scale, or softcap * tanh(q k^T * scale / softcap)
+  ALiBi:  + slope * col (pure causal), else - slope * |row + Sk - Sq - col|
+  masks:  col > row + (Sk - Sq) + wr (causal: wr = 0), col < row + (Sk - Sq) - wl
+  out = softmax(scores) v, lse = logsumexp(scores)
+GQA: KV head = query head // (Hq / Hk). Varlen runs the dense formula on each
+sequence slice given by cu_seqlens (device/varlen/mod.rs:79-136).
+
+Backward (device/backward/common.rs:121-152, dq.rs, dkv.rs, reduce.rs:40-108):
+  P = exp(scores - lse), dP = dO V^T, delta = rowsum(dO * O),
+  dS = P * (dP - delta) [* (1 - tanh^2) with softcap],
+  dV = P^T dO, dK = scale * dS^T Q, dQ = scale * dS K, with dK/dV summed over the
+  query heads of each KV head.
+
+Pins (tests/test_oracle_attention.py): torch's scaled_dot_product_attention and
+logsumexp on the CPU (a library routine), torch autograd of the same formula for
+the gradients, finite differences on tiny float64 cases, and closed forms:
+Sk = 1 gives O = V exactly, constant V rows give O = that row, all-zero Q gives
+LSE = log(#visible keys), empty / fully masked rows give O = 0 and LSE = +inf.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def _scores(q, k, scale, softcap, alibi_slopes, causal, wl, wr):
+    """q [B,Sq,H,D], k [B,Sk,Hk,D] -> scores [B,H,Sq,Sk] (masked entries -inf), and the
+    tanh values used by softcap (for the backward)."""
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    g = H // Hk
+    qh = np.transpose(q, (0, 2, 1, 3))  # B H Sq D
+    kh = np.repeat(np.transpose(k, (0, 2, 1, 3)), g, axis=1)  # B H Sk D
+    raw = qh @ np.swapaxes(kh, -1, -2)
+    t = None
+    if softcap and softcap > 0:
+        t = np.tanh(raw * (scale / softcap))
+        s = softcap * t
+    else:
+        s = raw * scale
+    off = Sk - Sq
+    rows = np.arange(Sq).reshape(Sq, 1)
+    cols = np.arange(Sk).reshape(1, Sk)
+    if alibi_slopes is not None:
+        slopes = np.asarray(alibi_slopes, dtype=s.dtype).reshape(-1, H, 1, 1)
+        if causal and wl < 0:
+            s = s + slopes * cols
+        else:
+            s = s - slopes * np.abs(rows + off - cols)
+    mask = np.zeros((Sq, Sk), dtype=bool)
+    if causal or wr >= 0:
+        mask |= cols > rows + off + (0 if causal else wr)
+    if wl >= 0:
+        mask |= cols < rows + off - wl
+    s = np.where(mask, -np.inf, s)
+    return s, t, mask
+
+
+def forward(q, k, v, *, softmax_scale=None, causal=False, window_left=-1, window_right=-1,
+            softcap=0.0, alibi_slopes=None, dtype=np.float32):
+    """Dense attention. q [B,Sq,H,D], k/v [B,Sk,Hk,D] -> out [B,Sq,H,D], lse [B,H,Sq]."""
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else softmax_scale
+    if Sk == 0:
+        return np.zeros_like(q), np.full((B, H, Sq), np.inf, dtype=dtype)
+    s, _, _ = _scores(q, k, scale, softcap, alibi_slopes, causal, window_left, window_right)
+    m = np.max(s, axis=-1, keepdims=True)
+    empty = ~np.isfinite(m)
+    m = np.where(empty, 0, m)
+    e = np.exp(s - m)
+    l = np.sum(e, axis=-1, keepdims=True)
+    p = np.where(l > 0, e / np.where(l > 0, l, 1), 0)
+    vh = np.repeat(np.transpose(v, (0, 2, 1, 3)), H // Hk, axis=1)
+    out = np.transpose(p @ vh, (0, 2, 1, 3))
+    lse = np.where(l[..., 0] > 0, m[..., 0] + np.log(np.where(l[..., 0] > 0, l[..., 0], 1)), np.inf)
+    return out.astype(dtype), lse.astype(dtype)
+
+
+def backward(q, k, v, out, dout, lse, *, softmax_scale=None, causal=False, window_left=-1,
+             window_right=-1, softcap=0.0, alibi_slopes=None, dtype=np.float32):
+    """Gradients of `forward`: returns dq [B,Sq,H,D], dk/dv [B,Sk,Hk,D] (GQA-summed)
+    and delta [B,H,Sq]."""
+    q, k, v, out, dout = (np.asarray(x, dtype=dtype) for x in (q, k, v, out, dout))
+    lse = np.asarray(lse, dtype=dtype)
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    g = H // Hk
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else softmax_scale
+    delta = np.sum(dout * out, axis=-1).transpose(0, 2, 1)  # B H Sq
+    if Sk == 0 or Sq == 0:
+        return np.zeros_like(q), np.zeros_like(k), np.zeros_like(v), delta
+    s, t, mask = _scores(q, k, scale, softcap, alibi_slopes, causal, window_left, window_right)
+    finite = np.isfinite(lse)[..., None]
+    p = np.where(finite & ~mask, np.exp(s - np.where(finite, lse[..., None], 0)), 0)
+    doh = np.transpose(dout, (0, 2, 1, 3))  # B H Sq D
+    qh = np.transpose(q, (0, 2, 1, 3))
+    kh = np.repeat(np.transpose(k, (0, 2, 1, 3)), g, axis=1)
+    vh = np.repeat(np.transpose(v, (0, 2, 1, 3)), g, axis=1)
+    dp = doh @ np.swapaxes(vh, -1, -2)
+    ds = p * (dp - delta[..., None])
+    if t is not None:
+        ds = ds * (1 - t * t)
+    dqh = scale * (ds @ kh)
+    dkh = scale * (np.swapaxes(ds, -1, -2) @ qh)
+    dvh = np.swapaxes(p, -1, -2) @ doh
+    dk = dkh.reshape(B, Hk, g, Sk, D).sum(axis=2)
+    dv = dvh.reshape(B, Hk, g, Sk, D).sum(axis=2)
+    return (np.transpose(dqh, (0, 2, 1, 3)).astype(dtype), np.transpose(dk, (0, 2, 1, 3)).astype(dtype),
+            np.transpose(dv, (0, 2, 1, 3)).astype(dtype), delta.astype(dtype))
+
+
+def _slices(cu):
+    cu = np.asarray(cu).tolist()
+    return [(cu[i], cu[i + 1]) for i in range(len(cu) - 1)]
+
+
+def varlen_forward(q, k, v, cu_q, cu_k, **kw):
+    """Packed attention: q [Tq,H,D], k/v [Tk,Hk,D] -> out [Tq,H,D], lse [H,Tq]."""
+    dtype = kw.get("dtype", np.float32)
+    q = np.asarray(q, dtype=dtype)
+    Tq, H, D = q.shape
+    out = np.zeros_like(q)
+    lse = np.full((H, Tq), np.inf, dtype=dtype)
+    alibi = kw.pop("alibi_slopes", None)
+    for b, ((qs, qe), (ks, ke)) in enumerate(zip(_slices(cu_q), _slices(cu_k))):
+        if qe == qs:
+            continue
+        slopes = None if alibi is None else (np.asarray(alibi)[b] if np.ndim(alibi) == 2 else alibi)
+        o, l = forward(q[None, qs:qe], np.asarray(k)[None, ks:ke], np.asarray(v)[None, ks:ke],
+                       alibi_slopes=slopes, **kw)
+        out[qs:qe] = o[0]
+        lse[:, qs:qe] = l[0]
+    return out, lse
+
+
+def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, **kw):
+    """Packed gradients: dq [Tq,H,D], dk/dv [Tk,Hk,D], delta [H, Tq + 128*B]: row r of
+    sequence b sits at column cu_q[b] + 128*b + r (device/varlen/backward.rs:126-131,
+    host/varlen/backward.rs:173-178); the padding columns are 0."""
+    dtype = kw.get("dtype", np.float32)
+    q, k, v, out, dout = (np.asarray(x, dtype=dtype) for x in (q, k, v, out, dout))
+    Tq, H, D = q.shape
+    nb = len(cu_q) - 1
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    delta = np.zeros((H, Tq + 128 * nb), dtype=dtype)
+    for b, ((qs, qe), (ks, ke)) in enumerate(zip(_slices(cu_q), _slices(cu_k))):
+        if qe == qs:
+            continue
+        a, b_, c, d = backward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke], out[None, qs:qe],
+                               dout[None, qs:qe], np.asarray(lse)[None, :, qs:qe], **kw)
+        dq[qs:qe] = a[0]
+        dk[ks:ke] += b_[0]
+        dv[ks:ke] += c[0]
+        delta[:, qs + 128 * b: qe + 128 * b] = d[0]
+    return dq, dk, dv, delta
