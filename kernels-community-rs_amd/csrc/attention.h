@@ -29,10 +29,31 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
     }
 }
 
-// Packs two f32 into the element type T (round to nearest even), lo in the low half.
+using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+using f16x2 = _Float16 __attribute__((ext_vector_type(2)));
+using f32x2 = float __attribute__((ext_vector_type(2)));
+
+// Packs two f32 into the element type T (round to nearest even), lo in the low
+// half: one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950.
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return Elem<T>::from_f32(lo) | (Elem<T>::from_f32(hi) << 16);
+    const f32x2 v = {lo, hi};
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+    }
+}
+
+// Buffer resource over `bytes` bytes at `base`: loads at offsets >= bytes return 0
+// (hardware range check), which zero-fills the tile rows past the sequence end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -29,30 +29,39 @@
 //   * Causal grids run the longest query tiles first, and the query heads sharing
 //     one KV head are placed on one XCD (blocks are dealt round-robin over the 8
 //     XCDs) so their K/V tiles hit the same L2.
+#include <cstdlib>
+
 #include "attention.h"
 
 namespace kcr {
 namespace attn {
 
 constexpr int kBN = 64;  // keys per tile
+constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag behind
 
+// GENERAL covers softcap, ALiBi and head sizes below the compiled bucket (zeroed
+// lanes of the padded head dimension); the fast path is the plain scaled dot
+// product with a positive scale.
 template <typename T, int D, int QT, int NW, bool VARLEN, bool GENERAL>
 __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
     constexpr int BN = kBN;
     constexpr int BM = 32 * QT * NW;
     constexpr int NT = NW * 64;
-    constexpr int KS = D / 16;  // MFMA k-steps over the head dim
-    constexpr int DB = D / 32;  // 32-wide blocks of the head dim in O
+    constexpr int KS = D / 16;   // MFMA k-steps over the head dim
+    constexpr int DB = D / 32;   // 32-wide blocks of the head dim in O
     constexpr int KSTR = D + 8;  // K tile row stride in LDS (elements)
-    constexpr int VSTR = BN + 8;  // V^T tile row stride in LDS (elements)
-    constexpr int DCH = D / 8;  // 16-byte chunks per row
+    constexpr int VSTR = BN + 8; // V^T tile row stride in LDS (elements)
+    constexpr int DCH = D / 8;   // 16-byte chunks per row
     constexpr int KCH = BN * DCH;
     constexpr int KPT = (KCH + NT - 1) / NT;
     constexpr int VIT = (BN / 4) * DCH;
     constexpr int VPT = (VIT + NT - 1) / NT;
+    constexpr int KTILE = BN * KSTR;
+    constexpr int VTILE = D * VSTR;
 
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * VSTR];
+    // Two stages of (K, V^T) so one barrier per key tile suffices.
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * KTILE];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * VTILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -139,7 +148,7 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int d0 = 16 * ks + 8 * hh;
-            if (row < sq && d0 < p.head_dim) {
+            if (row < sq && (!GENERAL || d0 < p.head_dim)) {
                 qf[qt][ks] = *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + d0);
             } else {
                 qf[qt][ks] = u32x4{0, 0, 0, 0};
@@ -151,6 +160,8 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
     if constexpr (GENERAL) {
         if (p.alibi) slope_log2 = p.alibi[b * p.alibi_b + head] * kLog2e;
     }
+    // Fast path: exp2(s * c - m) with the scale folded into one FMA.
+    const float c = GENERAL ? 1.0f : p.scale_log2;
 
     f32x16 o[QT][DB];
     float m[QT], l[QT];
@@ -162,83 +173,95 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
         for (int db = 0; db < DB; ++db) o[qt][db] = f32x16{};
     }
 
-    // ---- tile staging: HBM -> registers -> LDS ----
+    // ---- tile staging: HBM -> registers (buffer loads, rows past the end read
+    // as zero) -> LDS ----
     u32x4 kreg[KPT];
     u32x4 vreg[VPT][4];
+    const uint32_t krow_bytes = static_cast<uint32_t>(p.k_s) * 2u;
+    const uint32_t vrow_bytes = static_cast<uint32_t>(p.v_s) * 2u;
     auto load_tile = [&](int kb) {
+        // Valid bytes from the tile's first row: rows >= sk (and the padded head
+        // dims of the last row) fall outside the range and read as zero.
+        const int rows = min(sk - kb, BN);
+        const uint32_t kbytes = rows > 0 ? static_cast<uint32_t>((rows - 1) * p.k_s + p.head_dim) * 2u : 0u;
+        const uint32_t vbytes = rows > 0 ? static_cast<uint32_t>((rows - 1) * p.v_s + p.head_dim) * 2u : 0u;
+        const auto kr = make_rsrc(kbase + static_cast<int64_t>(kb) * p.k_s, kbytes);
+        const auto vr = make_rsrc(vbase + static_cast<int64_t>(kb) * p.v_s, vbytes);
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            const int c = tid + i * NT;
-            kreg[i] = u32x4{0, 0, 0, 0};
-            if (c < KCH) {
-                const int key = c / DCH;
-                const int dc = c - key * DCH;
-                const int gk = kb + key;
-                if (gk < sk && dc * 8 < p.head_dim) {
-                    kreg[i] = *reinterpret_cast<const u32x4*>(kbase + gk * p.k_s + dc * 8);
+            const int cidx = tid + i * NT;
+            if (KCH % NT == 0 || cidx < KCH) {
+                const int key = cidx / DCH;
+                const int dc = cidx - key * DCH;
+                kreg[i] = buffer_load16(kr, key * krow_bytes + dc * 16);
+                if constexpr (GENERAL) {
+                    if (dc * 8 >= p.head_dim) kreg[i] = u32x4{0, 0, 0, 0};
                 }
             }
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int it = tid + i * NT;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) vreg[i][e] = u32x4{0, 0, 0, 0};
-            if (it < VIT) {
+            if (VIT % NT == 0 || it < VIT) {
                 const int kq = it / DCH;
                 const int dc = it - kq * DCH;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int gk = kb + 4 * kq + e;
-                    if (gk < sk && dc * 8 < p.head_dim) {
-                        vreg[i][e] = *reinterpret_cast<const u32x4*>(vbase + gk * p.v_s + dc * 8);
+                    vreg[i][e] = buffer_load16(vr, (4 * kq + e) * vrow_bytes + dc * 16);
+                    if constexpr (GENERAL) {
+                        if (dc * 8 >= p.head_dim) vreg[i][e] = u32x4{0, 0, 0, 0};
                     }
                 }
             }
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int stage) {
+        uint16_t* kl = k_lds + stage * KTILE;
+        uint16_t* vl = v_lds + stage * VTILE;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            const int c = tid + i * NT;
-            if (c < KCH) {
-                const int key = c / DCH;
-                const int dc = c - key * DCH;
-                *reinterpret_cast<u32x4*>(&k_lds[key * KSTR + dc * 8]) = kreg[i];
+            const int cidx = tid + i * NT;
+            if (KCH % NT == 0 || cidx < KCH) {
+                const int key = cidx / DCH;
+                const int dc = cidx - key * DCH;
+                *reinterpret_cast<u32x4*>(&kl[key * KSTR + dc * 8]) = kreg[i];
             }
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int it = tid + i * NT;
-            if (it < VIT) {
+            if (VIT % NT == 0 || it < VIT) {
                 const int kq = it / DCH;
                 const int dc = it - kq * DCH;
+                // 4 keys x 8 d -> eight 8-byte rows of V^T (byte permutes).
 #pragma unroll
-                for (int dd = 0; dd < 8; ++dd) {
-                    const int w = dd >> 1;
-                    const int sh = (dd & 1) * 16;
-                    const uint32_t e0 = (vreg[i][0][w] >> sh) & 0xffffu;
-                    const uint32_t e1 = (vreg[i][1][w] >> sh) & 0xffffu;
-                    const uint32_t e2 = (vreg[i][2][w] >> sh) & 0xffffu;
-                    const uint32_t e3 = (vreg[i][3][w] >> sh) & 0xffffu;
-                    uint2 packed;
-                    packed.x = e0 | (e1 << 16);
-                    packed.y = e2 | (e3 << 16);
-                    *reinterpret_cast<uint2*>(&v_lds[(8 * dc + dd) * VSTR + 4 * kq]) = packed;
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t a0 = vreg[i][0][w], a1 = vreg[i][1][w];
+                    const uint32_t a2 = vreg[i][2][w], a3 = vreg[i][3][w];
+                    uint2 lo, hi;  // d = 2w (low halves) and d = 2w + 1 (high halves)
+                    lo.x = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+                    lo.y = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+                    hi.x = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+                    hi.y = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
+                    *reinterpret_cast<uint2*>(&vl[(8 * dc + 2 * w) * VSTR + 4 * kq]) = lo;
+                    *reinterpret_cast<uint2*>(&vl[(8 * dc + 2 * w + 1) * VSTR + 4 * kq]) = hi;
                 }
             }
         }
     };
 
-    if (kv_begin < kv_end) {
+    const int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
+    if (ntiles > 0) {
         load_tile(kv_begin);
-        store_tile();
+        store_tile(0);
+        if (ntiles > 1) load_tile(kv_begin + BN);
         __syncthreads();
     }
 
-    for (int kb = kv_begin; kb < kv_end; kb += BN) {
-        const bool has_next = kb + BN < kv_end;
-        if (has_next) load_tile(kb + BN);
+    for (int t = 0; t < ntiles; ++t) {
+        const int kb = kv_begin + t * BN;
+        const uint16_t* kl = k_lds + (t & 1) * KTILE;
+        const uint16_t* vl = v_lds + (t & 1) * VTILE;
 
         // ---- S^T = K Q^T for 64 keys x 32*QT queries ----
         f32x16 s[QT][2];
@@ -249,9 +272,8 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(&k_lds[l32 * KSTR + 16 * ks + 8 * hh]);
-            const u32x4 ka1 =
-                *reinterpret_cast<const u32x4*>(&k_lds[(32 + l32) * KSTR + 16 * ks + 8 * hh]);
+            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(&kl[l32 * KSTR + 16 * ks + 8 * hh]);
+            const u32x4 ka1 = *reinterpret_cast<const u32x4*>(&kl[(32 + l32) * KSTR + 16 * ks + 8 * hh]);
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
                 s[qt][0] = mfma32<T>(ka0, qf[qt][ks], s[qt][0]);
@@ -259,21 +281,27 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
             }
         }
 
-        // ---- scores (log2 domain), masks, online softmax ----
+        // The next tile's registers go to the other LDS stage while this one is
+        // consumed; its last readers finished before the previous barrier.
+        if (t + 1 < ntiles) {
+            store_tile((t + 1) & 1);
+            if (t + 2 < ntiles) load_tile(kb + 2 * BN);
+        }
+
+        // ---- scores, masks, online softmax (lazy rescale) ----
         const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
                                (wl >= 0 && kb < last_row + off - wl);
         u32x4 pk[QT][4];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const int row = wrow0 + qt * 32 + l32;
-            float mx = -INFINITY;
+            if constexpr (GENERAL) {
 #pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
+                for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float x = s[qt][sub][r];
-                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if constexpr (GENERAL) {
+                    for (int r = 0; r < 16; ++r) {
+                        const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        float x = s[qt][sub][r];
                         if (p.tanh_scale > 0.0f) {
                             x = tanhf(x * p.tanh_scale) * p.scale_eff_log2;
                         } else {
@@ -283,43 +311,59 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
                             x += p.alibi_causal ? slope_log2 * static_cast<float>(col)
                                                 : -slope_log2 * fabsf(static_cast<float>(row + off - col));
                         }
-                    } else {
-                        x *= p.scale_log2;
+                        s[qt][sub][r] = x;
                     }
-                    if (need_mask) {
-                        const bool masked = (col >= sk) || (wr >= 0 && col > row + off + wr) ||
-                                            (wl >= 0 && col < row + off - wl);
-                        if (masked) x = -INFINITY;
-                    }
-                    s[qt][sub][r] = x;
-                    mx = fmaxf(mx, x);
                 }
             }
+            if (need_mask) {
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        const bool masked = (col >= sk) || (wr >= 0 && col > row + off + wr) ||
+                                            (wl >= 0 && col < row + off - wl);
+                        s[qt][sub][r] = masked ? -INFINITY : s[qt][sub][r];
+                    }
+                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[qt][sub][r], s[qt][sub][r + 1]));
+            }
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m[qt], mx);
-            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-            const float alpha = fast_exp2(m[qt] - m_use);
-            m[qt] = m_new;
+            const float m2 = mx * c;
+            // Rescale O and l only when some row's max grew by more than the slack:
+            // exp2(s*c - m) then stays <= 2^slack, which bf16 P and f32 sums hold.
+            if (__any(m2 > m[qt] + kRescaleSlack)) {
+                const float m_new = fmaxf(m[qt], m2);
+                const float alpha = (m_new == -INFINITY) ? 1.0f : fast_exp2(m[qt] - m_new);
+                m[qt] = m_new;
+                l[qt] *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) o[qt][db] *= alpha;
+            }
+            const float neg_m = (m[qt] == -INFINITY) ? 0.0f : -m[qt];
             float rowsum = 0.0f;
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float pv = fast_exp2(s[qt][sub][r] - m_use);
+                    const float pv = fast_exp2(__builtin_fmaf(s[qt][sub][r], c, neg_m));
                     s[qt][sub][r] = pv;
                     rowsum += pv;
                 }
             }
-            l[qt] = l[qt] * alpha + rowsum;
+            l[qt] += rowsum;
 #pragma unroll
-            for (int db = 0; db < DB; ++db) o[qt][db] *= alpha;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int sub = t >> 1;
-                const int base = 8 * (t & 1);
+            for (int tt = 0; tt < 4; ++tt) {
+                const int sub = tt >> 1;
+                const int base = 8 * (tt & 1);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    pk[qt][t][w] = pack2<T>(s[qt][sub][base + 2 * w], s[qt][sub][base + 2 * w + 1]);
+                    pk[qt][tt][w] = pack2<T>(s[qt][sub][base + 2 * w], s[qt][sub][base + 2 * w + 1]);
                 }
             }
         }
@@ -328,21 +372,16 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint16_t* vrow = &v_lds[(32 * db + l32) * VSTR + 16 * t + 4 * hh];
+            for (int tt = 0; tt < 4; ++tt) {
+                const uint16_t* vrow = &vl[(32 * db + l32) * VSTR + 16 * tt + 4 * hh];
                 const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
                 const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
                 const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
-                for (int qt = 0; qt < QT; ++qt) o[qt][db] = mfma32<T>(va, pk[qt][t], o[qt][db]);
+                for (int qt = 0; qt < QT; ++qt) o[qt][db] = mfma32<T>(va, pk[qt][tt], o[qt][db]);
             }
         }
-
         __syncthreads();
-        if (has_next) {
-            store_tile();
-            __syncthreads();
-        }
     }
 
     // ---- epilogue: O / l, LSE = (m + log2 l) * ln 2 (forward/mod.rs:846-865) ----
@@ -358,7 +397,7 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d = 32 * db + 8 * g + 4 * hh;
-                if (d < p.head_dim) {
+                if (!GENERAL || d < p.head_dim) {
                     uint2 w;
                     w.x = pack2<T>(o[qt][db][4 * g] * inv, o[qt][db][4 * g + 1] * inv);
                     w.y = pack2<T>(o[qt][db][4 * g + 2] * inv, o[qt][db][4 * g + 3] * inv);
@@ -437,8 +476,23 @@ void launch_cfg(FwdParams& prm, bool general, hipStream_t s) {
     check_launch("launch flash_fwd");
 }
 
+int tile_override() {
+    static const int v = [] {
+        const char* e = std::getenv("KCR_FA_FWD_TILE");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
 template <typename T, int D, bool VARLEN>
 void launch_d(FwdParams& prm, bool general, hipStream_t s) {
+    if constexpr (D == 128) {
+        switch (tile_override()) {
+            case 24: return launch_cfg<T, D, 2, 4, VARLEN>(prm, general, s);
+            case 22: return launch_cfg<T, D, 2, 2, VARLEN>(prm, general, s);
+            default: break;
+        }
+    }
     launch_cfg<T, D, 1, 4, VARLEN>(prm, general, s);
 }
 
@@ -481,6 +535,18 @@ void check_alibi(const kcr_tensor* alibi, int64_t b, int64_t h, int32_t& alibi_b
                           std::to_string(b) + ", " + std::to_string(h) + "]");
     }
     require_device(alibi, "alibi_slopes");
+}
+
+// The tile loads bound each K/V tile by its row count: rows must not overlap
+// (sequence stride >= head size) and 64 rows must span less than 2 GiB.
+void check_kv_rows(const kcr_tensor* k, const kcr_tensor* v, int seq_dim, int64_t d) {
+    for (auto* t : {k, v}) {
+        const int64_t s = t->strides[seq_dim];
+        if (t->shape[seq_dim] > 1 && (s < d || s > (int64_t{1} << 23))) {
+            throw value_error("k and v rows must not overlap (sequence stride >= head size) and the "
+                              "sequence stride must be at most 2^23 elements");
+        }
+    }
 }
 
 void check_head_dim(int64_t d) {
@@ -541,6 +607,7 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
                 throw value_error("q, k, v and out must have 16-byte aligned rows (strides multiple of 8 elements)");
             }
         }
+        check_kv_rows(k, v, 1, D);
         require_device(q, "q");
         require_device(k, "k");
         require_device(v, "v");
@@ -588,7 +655,7 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         prm.scale_log2 = opt.scale * kLog2e;
         prm.tanh_scale = opt.tanh_scale;
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
-        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr;
+        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<false>(prm, q->dtype, bucket_for(D), general, s);
     });
 }
@@ -647,6 +714,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
                 throw value_error("q, k, v and out must have 16-byte aligned rows (strides multiple of 8 elements)");
             }
         }
+        check_kv_rows(k, v, 0, D);
         require_device(q, "q");
         require_device(k, "k");
         require_device(v, "v");
@@ -697,7 +765,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         prm.scale_log2 = opt.scale * kLog2e;
         prm.tanh_scale = opt.tanh_scale;
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
-        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr;
+        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<true>(prm, q->dtype, bucket_for(D), general, s);
     });
 }

@@ -44,7 +44,9 @@ def _packed(t):
     """A 16-byte aligned view of `t` with unit last stride (repacked if needed)."""
     if t is None or t.numel() == 0:
         return t
-    if t.stride(-1) == 1 and _rows_aligned(t):
+    # Rows of one sequence position must not overlap (e.g. broadcast views).
+    if t.stride(-1) == 1 and _rows_aligned(t) and (t.ndim < 3 or t.shape[-3] <= 1
+                                                    or t.stride(-3) >= t.shape[-1]):
         return t
     return t.clone(memory_format=torch.contiguous_format)
 
