@@ -37,13 +37,23 @@ namespace kcr {
 namespace attn {
 
 constexpr int kBN = 64;  // keys per tile
+
+// V^T tile rows hold 16 chunks of 4 keys (8 bytes). The loading threads write
+// one chunk to each of 16 rows that are 8 apart; XOR-ing the chunk index with
+// bits of (row / 16) spreads those writes over distinct LDS banks. Bit 1 of
+// the chunk index is left alone so the two chunks an MFMA operand needs
+// (chunks c and c + 2) stay a constant 16 bytes apart.
+__device__ __forceinline__ int vt_swizzle(int row) {
+    const int x = (row >> 4) & 7;
+    return (x & 1) | ((x & 6) << 1);
+}
 constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag behind
 
 // GENERAL covers softcap, ALiBi and head sizes below the compiled bucket (zeroed
 // lanes of the padded head dimension); the fast path is the plain scaled dot
 // product with a positive scale.
 template <typename T, int D, int QT, int NW, bool VARLEN, bool GENERAL>
-__global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(const FwdParams p) {
     constexpr int BN = kBN;
     constexpr int BM = 32 * QT * NW;
     constexpr int NT = NW * 64;
@@ -243,8 +253,9 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
                     lo.y = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
                     hi.x = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
                     hi.y = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-                    *reinterpret_cast<uint2*>(&vl[(8 * dc + 2 * w) * VSTR + 4 * kq]) = lo;
-                    *reinterpret_cast<uint2*>(&vl[(8 * dc + 2 * w + 1) * VSTR + 4 * kq]) = hi;
+                    const int r0 = 8 * dc + 2 * w;
+                    *reinterpret_cast<uint2*>(&vl[r0 * VSTR + 4 * (kq ^ vt_swizzle(r0))]) = lo;
+                    *reinterpret_cast<uint2*>(&vl[(r0 + 1) * VSTR + 4 * (kq ^ vt_swizzle(r0 + 1))]) = hi;
                 }
             }
         }
@@ -373,7 +384,8 @@ __global__ void __launch_bounds__(NW * 64) flash_fwd_kernel(const FwdParams p) {
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
-                const uint16_t* vrow = &vl[(32 * db + l32) * VSTR + 16 * tt + 4 * hh];
+                const int vr = 32 * db + l32;
+                const uint16_t* vrow = &vl[vr * VSTR + 4 * ((4 * tt + hh) ^ vt_swizzle(vr))];
                 const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
                 const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
                 const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
