@@ -145,7 +145,10 @@ template <>
 struct Elem<bf16_t> {
     using storage = uint16_t;
     static __device__ __forceinline__ float to_f32(uint32_t bits) { return bf16_bits_to_f32(bits); }
-    static __device__ __forceinline__ uint32_t from_f32(float v) { return f32_to_bf16_bits(v); }
+    // Round to nearest even (v_cvt_pk_bf16_f32).
+    static __device__ __forceinline__ uint32_t from_f32(float v) {
+        return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+    }
     static __device__ __forceinline__ float load(const bf16_t* p) { return to_f32(p->bits); }
     static __device__ __forceinline__ void store(bf16_t* p, float v) {
         p->bits = static_cast<uint16_t>(from_f32(v));
@@ -179,13 +182,26 @@ __device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
     }
 }
 
+// Two f32 -> one word of two 16-bit elements (lo in the low half), round to
+// nearest even: a single v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950.
+template <typename T>
+__device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
+    using f32x2 = float __attribute__((ext_vector_type(2)));
+    const f32x2 v = {lo, hi};
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    } else {
+        using f16x2 = _Float16 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
     u32x4 w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        w[i] = Elem<T>::from_f32(f[2 * i]) | (Elem<T>::from_f32(f[2 * i + 1]) << 16);
-    }
+    for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(f[2 * i], f[2 * i + 1]);
     return w;
 }
 

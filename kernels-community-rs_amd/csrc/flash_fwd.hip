@@ -421,6 +421,315 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     }
 }
 
+// ---------------------------------------------------------------------------
+// Forward v3 (plain scaled dot product, head size 64 or 128): K and V tiles are
+// copied HBM -> LDS by direct buffer loads (no staging registers, no VALU),
+// both row-major with an XOR swizzle of the 16-byte chunks within a row:
+//   * K is read as the A operand of S^T = K Q^T with ds_read_b128,
+//   * V^T, the A operand of O^T = V^T P^T, is read with ds_read_b64_tr_b16,
+//     which transposes 4 rows x 16 columns of 16-bit values inside each group
+//     of 16 lanes (lane i receives column i of the 4 rows).
+// swz(row) sends the 8 (or 16) consecutive rows of a ds_read_b128 phase and the
+// 4 consecutive rows x 2 chunks of a transposing read to distinct banks.
+// Two LDS stages; the next tile's copy is in flight during the current tile.
+// ---------------------------------------------------------------------------
+template <int CH>
+__device__ __forceinline__ int kv_swizzle(int row) {
+    // CH chunks of 16 bytes per row (CH = 8 or 16).
+    return ((row & (CH / 2 - 1)) << 1) | ((row / (CH / 2)) & 1);
+}
+
+using s16x4 = short __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// 16 bytes per lane from `r` at byte `voffset` into LDS at lds_base + 16 * lane.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, const uint16_t* lds_base,
+                                           uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maximum).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <typename T, int D, int QT, int NW, bool VARLEN>
+__global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParams p) {
+    constexpr int BN = kBN;
+    constexpr int BM = 32 * QT * NW;
+    constexpr int KS = D / 16;
+    constexpr int DB = D / 32;
+    constexpr int CH = D / 8;            // 16-byte chunks per row
+    constexpr int ROW = D;               // LDS row stride (elements), no padding
+    constexpr int TILE = BN * ROW;       // elements per K or V tile
+    constexpr int INSTS = BN * CH / 64;  // wave-wide 1 KB copies per tile
+    constexpr int IPW = INSTS / NW;      // ... per wave
+    static_assert(INSTS % NW == 0, "tile copies must split evenly over the waves");
+
+    __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2 * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2 * TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;
+
+    const int per_tile = p.batch * p.heads;
+    const int qo = blockIdx.x / per_tile;
+    const int rem = blockIdx.x - qo * per_tile;
+    int bh;
+    if (p.xcd_groups) {
+        const int xcd = rem & 7;
+        const int rr = rem >> 3;
+        const int j = rr % p.gqa;
+        const int g = (rr / p.gqa) * 8 + xcd;
+        bh = g * p.gqa + j;
+    } else {
+        bh = rem;
+    }
+    const int b = bh / p.heads;
+    const int head = bh - b * p.heads;
+    const int kvh = head / p.gqa;
+    const int qb = p.q_blocks - 1 - qo;
+
+    int64_t q_off = 0, k_off = 0;
+    int sq = p.seqlen_q, sk = p.seqlen_k;
+    int lse_row0 = 0;
+    if constexpr (VARLEN) {
+        const int qs = p.cu_q[b];
+        const int qe = p.cu_q[b + 1];
+        const int ks = p.cu_k[b];
+        const int ke = p.cu_k[b + 1];
+        const int len = p.seqused_k ? p.seqused_k[b] : ke - ks;
+        const int pad = p.leftpad_k ? p.leftpad_k[b] : 0;
+        if (qs < 0 || qe < qs || qe > p.total_q || ks < 0 || ke < ks || ke > p.total_k || pad < 0 ||
+            len < pad || len > ke - ks || qe - qs > p.seqlen_q) {
+            return;
+        }
+        sq = qe - qs;
+        sk = len - pad;
+        q_off = static_cast<int64_t>(qs);
+        k_off = static_cast<int64_t>(ks + pad);
+        lse_row0 = qs;
+    }
+    const int row0 = qb * BM;
+    if (row0 >= sq) return;
+    const int off = sk - sq;
+    const int wl = p.window_left;
+    const int wr = p.window_right;
+
+    const uint16_t* qbase;
+    const uint16_t* kbase;
+    const uint16_t* vbase;
+    uint16_t* obase;
+    if constexpr (VARLEN) {
+        qbase = static_cast<const uint16_t*>(p.q) + q_off * p.q_s + head * p.q_h;
+        kbase = static_cast<const uint16_t*>(p.k) + k_off * p.k_s + kvh * p.k_h;
+        vbase = static_cast<const uint16_t*>(p.v) + k_off * p.v_s + kvh * p.v_h;
+        obase = static_cast<uint16_t*>(p.o) + q_off * p.o_s + head * p.o_h;
+    } else {
+        qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
+        kbase = static_cast<const uint16_t*>(p.k) + b * p.k_b + kvh * p.k_h;
+        vbase = static_cast<const uint16_t*>(p.v) + b * p.v_b + kvh * p.v_h;
+        obase = static_cast<uint16_t*>(p.o) + b * p.o_b + head * p.o_h;
+    }
+    float* lse_base = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + lse_row0;
+
+    const int last_row = min(row0 + BM, sq) - 1;
+    int kv_end = sk;
+    if (wr >= 0) kv_end = max(0, min(sk, last_row + 1 + off + wr));
+    int kv_begin = 0;
+    if (wl >= 0) kv_begin = (max(0, min(sk, row0 + off - wl)) / BN) * BN;
+
+    const int wrow0 = row0 + wave * 32 * QT;
+    u32x4 qf[QT][KS];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int row = wrow0 + qt * 32 + l32;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            qf[qt][ks] = row < sq ? *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + 16 * ks + 8 * hh)
+                                  : u32x4{0, 0, 0, 0};
+        }
+    }
+    const float c = p.scale_log2;
+
+    f32x16 o[QT][DB];
+    float m[QT], l[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[qt][db] = f32x16{};
+    }
+
+    // Per-lane source offsets of this wave's tile copies (constant across tiles).
+    uint32_t k_src[IPW], v_src[IPW];
+    const uint32_t krow_bytes = static_cast<uint32_t>(p.k_s) * 2u;
+    const uint32_t vrow_bytes = static_cast<uint32_t>(p.v_s) * 2u;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        const int chunk = (wave * IPW + i) * 64 + lane;  // LDS chunk this lane fills
+        const int row = chunk / CH;
+        const int gc = (chunk % CH) ^ kv_swizzle<CH>(row);
+        k_src[i] = row * krow_bytes + gc * 16;
+        v_src[i] = row * vrow_bytes + gc * 16;
+    }
+    auto copy_tile = [&](int kb, int stage) {
+        const int rows = min(sk - kb, BN);
+        const uint32_t kbytes = static_cast<uint32_t>((rows - 1) * p.k_s + D) * 2u;
+        const uint32_t vbytes = static_cast<uint32_t>((rows - 1) * p.v_s + D) * 2u;
+        const auto kr = make_rsrc(kbase + static_cast<int64_t>(kb) * p.k_s, kbytes);
+        const auto vr = make_rsrc(vbase + static_cast<int64_t>(kb) * p.v_s, vbytes);
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            const int base = (wave * IPW + i) * 64 * 8;  // elements
+            load_lds16(kr, k_lds + stage * TILE + base, k_src[i]);
+            load_lds16(vr, v_lds + stage * TILE + base, v_src[i]);
+        }
+    };
+
+    const int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
+    if (ntiles > 0) {
+        copy_tile(kv_begin, 0);
+        wait_vmem();
+        __syncthreads();
+    }
+
+    // Lane-constant parts of the LDS read addresses.
+    const int g16 = (lane >> 4) & 1;  // which 16 of the 32 d in an O^T block
+    const int li = lane & 15;
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int kb = kv_begin + t * BN;
+        const uint16_t* kl = k_lds + (t & 1) * TILE;
+        const uint16_t* vl = v_lds + (t & 1) * TILE;
+        if (t + 1 < ntiles) copy_tile(kb + BN, (t + 1) & 1);
+
+        f32x16 s[QT][2];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            s[qt][0] = f32x16{};
+            s[qt][1] = f32x16{};
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int c0 = 2 * ks + hh;
+            const int r0 = l32, r1 = 32 + l32;
+            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(&kl[r0 * ROW + 8 * (c0 ^ kv_swizzle<CH>(r0))]);
+            const u32x4 ka1 = *reinterpret_cast<const u32x4*>(&kl[r1 * ROW + 8 * (c0 ^ kv_swizzle<CH>(r1))]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                s[qt][0] = mfma32<T>(ka0, qf[qt][ks], s[qt][0]);
+                s[qt][1] = mfma32<T>(ka1, qf[qt][ks], s[qt][1]);
+            }
+        }
+
+        const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
+                               (wl >= 0 && kb < last_row + off - wl);
+        u32x4 pk[QT][4];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const int row = wrow0 + qt * 32 + l32;
+            if (need_mask) {
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        const bool masked = (col >= sk) | (wr >= 0 & col > row + off + wr) |
+                                            (wl >= 0 & col < row + off - wl);
+                        s[qt][sub][r] = masked ? -INFINITY : s[qt][sub][r];
+                    }
+                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[qt][sub][r], s[qt][sub][r + 1]));
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m2 = mx * c;
+            if (__any(m2 > m[qt] + kRescaleSlack)) {
+                const float m_new = fmaxf(m[qt], m2);
+                const float alpha = (m_new == -INFINITY) ? 1.0f : fast_exp2(m[qt] - m_new);
+                m[qt] = m_new;
+                l[qt] *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) o[qt][db] *= alpha;
+            }
+            const float neg_m = (m[qt] == -INFINITY) ? 0.0f : -m[qt];
+            float rowsum = 0.0f;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = fast_exp2(__builtin_fmaf(s[qt][sub][r], c, neg_m));
+                    s[qt][sub][r] = pv;
+                    rowsum += pv;
+                }
+            }
+            l[qt] += rowsum;
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const int sub = tt >> 1;
+                const int base = 8 * (tt & 1);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    pk[qt][tt][w] = pack2<T>(s[qt][sub][base + 2 * w], s[qt][sub][base + 2 * w + 1]);
+                }
+            }
+        }
+
+        // ---- O^T += V^T P^T, V^T read transposed from the row-major tile ----
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int gc = 4 * db + 2 * g16 + ((li & 3) >> 1);
+            const int half = 4 * (li & 1);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const int ra = 16 * tt + 4 * hh + (li >> 2);
+                const int rb = ra + 8;
+                const uint2 lo = ds_read_tr16(&vl[ra * ROW + 8 * (gc ^ kv_swizzle<CH>(ra)) + half]);
+                const uint2 hi = ds_read_tr16(&vl[rb * ROW + 8 * (gc ^ kv_swizzle<CH>(rb)) + half]);
+                const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][db] = mfma32<T>(va, pk[qt][tt], o[qt][db]);
+            }
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int row = wrow0 + qt * 32 + l32;
+        const float lt = l[qt] + __shfl_xor(l[qt], 32, 64);
+        if (row >= sq) continue;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        uint16_t* orow = obase + row * p.o_s;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * hh;
+                uint2 w;
+                w.x = pack2<T>(o[qt][db][4 * g] * inv, o[qt][db][4 * g + 1] * inv);
+                w.y = pack2<T>(o[qt][db][4 * g + 2] * inv, o[qt][db][4 * g + 3] * inv);
+                *reinterpret_cast<uint2*>(orow + d) = w;
+            }
+        }
+        if (hh == 0) lse_base[row] = lt > 0.0f ? (m[qt] + fast_log2(lt)) * kLn2 : INFINITY;
+    }
+}
+
 // Empty-key rows: O = 0, LSE = +inf (host/forward/mod.rs:548-572). Also clears
 // the output when zero_tensors is requested. Uses kernels rather than
 // hipMemsetAsync so the calls stay safe inside captured graphs.
@@ -496,13 +805,27 @@ int tile_override() {
     return v;
 }
 
+template <typename T, int D, int QT, int NW, bool VARLEN>
+void launch_v3(FwdParams& prm, hipStream_t s) {
+    constexpr int BM = 32 * QT * NW;
+    prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
+    const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads;
+    if (blocks == 0) return;
+    if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
+    prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
+    flash_fwd_v3_kernel<T, D, QT, NW, VARLEN><<<static_cast<unsigned>(blocks), NW * 64, 0, s>>>(prm);
+    check_launch("launch flash_fwd");
+}
+
 template <typename T, int D, bool VARLEN>
 void launch_d(FwdParams& prm, bool general, hipStream_t s) {
-    if constexpr (D == 128) {
-        switch (tile_override()) {
-            case 24: return launch_cfg<T, D, 2, 4, VARLEN>(prm, general, s);
-            case 22: return launch_cfg<T, D, 2, 2, VARLEN>(prm, general, s);
-            default: break;
+    if constexpr (D == 64 || D == 128) {
+        if (!general) {
+            switch (tile_override()) {
+                case 1: break;  // the v2 kernel
+                case 24: return launch_v3<T, D, 2, 4, VARLEN>(prm, s);
+                default: return launch_v3<T, D, 1, 4, VARLEN>(prm, s);
+            }
         }
     }
     launch_cfg<T, D, 1, 4, VARLEN>(prm, general, s);

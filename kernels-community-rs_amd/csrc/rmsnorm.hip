@@ -62,8 +62,7 @@ __device__ __forceinline__ u32x4 narrow16(const float* f) {
         for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(f[i]);
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = Elem<T>::from_f32(f[2 * i]) | (Elem<T>::from_f32(f[2 * i + 1]) << 16);
+        for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(f[2 * i], f[2 * i + 1]);
     }
     return w;
 }
