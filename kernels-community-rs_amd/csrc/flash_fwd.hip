@@ -423,22 +423,21 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 
 // ---------------------------------------------------------------------------
 // Forward v3 (plain scaled dot product, head size 64 or 128): K and V tiles are
-// copied HBM -> LDS by direct buffer loads (no staging registers, no VALU),
-// both row-major with an XOR swizzle of the 16-byte chunks within a row:
-//   * K is read as the A operand of S^T = K Q^T with ds_read_b128,
+// copied HBM -> LDS by direct buffer loads (no staging registers, no VALU).
+// LDS layout "4-key blocks": each wave-wide 16-byte-per-lane copy moves four
+// whole rows (keys 4j..4j+3, coalesced in HBM) into one block, stored
+// chunk-major inside the block (chunk c of key 4j+i at c*64 + 16*i bytes);
+// blocks are padded by 64 bytes. Then
+//   * K, the A operand of S^T = K Q^T, is one ds_read_b128 per operand at
+//     lane_base + immediate,
 //   * V^T, the A operand of O^T = V^T P^T, is read with ds_read_b64_tr_b16,
 //     which transposes 4 rows x 16 columns of 16-bit values inside each group
-//     of 16 lanes (lane i receives column i of the 4 rows).
-// swz(row) sends the 8 (or 16) consecutive rows of a ds_read_b128 phase and the
-// 4 consecutive rows x 2 chunks of a transposing read to distinct banks.
+//     of 16 lanes (lane i receives column i of the 4 rows): a group's 4 keys are
+//     one block and its two chunks are 128 contiguous bytes,
+// so no read needs per-tile address arithmetic and none conflicts on banks
+// (the padding puts neighbouring blocks 16 banks apart).
 // Two LDS stages; the next tile's copy is in flight during the current tile.
 // ---------------------------------------------------------------------------
-template <int CH>
-__device__ __forceinline__ int kv_swizzle(int row) {
-    // CH chunks of 16 bytes per row (CH = 8 or 16).
-    return ((row & (CH / 2 - 1)) << 1) | ((row / (CH / 2)) & 1);
-}
-
 using s16x4 = short __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
@@ -449,26 +448,44 @@ __device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
 
 // 16 bytes per lane from `r` at byte `voffset` into LDS at lds_base + 16 * lane.
 __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, const uint16_t* lds_base,
-                                           uint32_t voffset) {
+                                           uint32_t voffset, uint32_t soffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset, 0, 0, 0);
+        r, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset, soffset, 0, 0);
 }
 
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maximum).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <typename T, int D, int QT, int NW, bool VARLEN>
+template <int CH>
+__device__ __forceinline__ int kv_swizzle(int row) {
+    // XOR swizzle of the 16-byte chunks of a row-major tile row (CH = 8 or 16).
+    return ((row & (CH / 2 - 1)) << 1) | ((row / (CH / 2)) & 1);
+}
+
+// LAYOUT 1: 4-key blocks (above). LAYOUT 0: row-major rows with the chunks of
+// each row XOR-swizzled by kv_swizzle (one 1 KB copy = 4 rows; addresses of the
+// reads need per-lane XOR arithmetic).
+template <typename T, int D, int QT, int NW, bool VARLEN, int LAYOUT>
 __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParams p) {
     constexpr int BN = kBN;
     constexpr int BM = 32 * QT * NW;
     constexpr int KS = D / 16;
     constexpr int DB = D / 32;
-    constexpr int CH = D / 8;            // 16-byte chunks per row
-    constexpr int ROW = D;               // LDS row stride (elements), no padding
-    constexpr int TILE = BN * ROW;       // elements per K or V tile
-    constexpr int INSTS = BN * CH / 64;  // wave-wide 1 KB copies per tile
-    constexpr int IPW = INSTS / NW;      // ... per wave
-    static_assert(INSTS % NW == 0, "tile copies must split evenly over the waves");
+    constexpr int CH = D / 8;               // 16-byte chunks per row
+    constexpr int KPB = 64 / CH;            // keys per 1 KB block (4 for D = 128)
+    constexpr int BLK = LAYOUT == 0 ? 512 : 512 + 32;  // block stride (elements): 1 KB (+ 64 B)
+    constexpr int NBLK = BN / KPB;          // blocks per tile
+    constexpr int TILE = NBLK * BLK;        // elements per K or V tile
+    constexpr int IPW = NBLK / NW;          // blocks each wave copies per tile
+    static_assert(NBLK % NW == 0, "tile blocks must split evenly over the waves");
+    // Element offset of (key, chunk c) in a tile.
+    auto kv_at = [](int key, int c) {
+        if constexpr (LAYOUT == 0) {
+            return key * D + 8 * (c ^ kv_swizzle<CH>(key));
+        } else {
+            return (key / KPB) * BLK + c * (8 * KPB) + 8 * (key % KPB);
+        }
+    };
 
     __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2 * TILE];
     __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2 * TILE];
@@ -569,18 +586,13 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
         for (int db = 0; db < DB; ++db) o[qt][db] = f32x16{};
     }
 
-    // Per-lane source offsets of this wave's tile copies (constant across tiles).
-    uint32_t k_src[IPW], v_src[IPW];
+    // Lane i of a block copy moves chunk i / KPB of key i % KPB; the block's
+    // first row goes in the scalar offset.
     const uint32_t krow_bytes = static_cast<uint32_t>(p.k_s) * 2u;
     const uint32_t vrow_bytes = static_cast<uint32_t>(p.v_s) * 2u;
-#pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-        const int chunk = (wave * IPW + i) * 64 + lane;  // LDS chunk this lane fills
-        const int row = chunk / CH;
-        const int gc = (chunk % CH) ^ kv_swizzle<CH>(row);
-        k_src[i] = row * krow_bytes + gc * 16;
-        v_src[i] = row * vrow_bytes + gc * 16;
-    }
+    // (LAYOUT 0 recomputes the swizzled source chunk per block in copy_tile.)
+    const uint32_t k_src = static_cast<uint32_t>(lane % KPB) * krow_bytes + (lane / KPB) * 16u;
+    const uint32_t v_src = static_cast<uint32_t>(lane % KPB) * vrow_bytes + (lane / KPB) * 16u;
     auto copy_tile = [&](int kb, int stage) {
         const int rows = min(sk - kb, BN);
         const uint32_t kbytes = static_cast<uint32_t>((rows - 1) * p.k_s + D) * 2u;
@@ -589,9 +601,16 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
         const auto vr = make_rsrc(vbase + static_cast<int64_t>(kb) * p.v_s, vbytes);
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
-            const int base = (wave * IPW + i) * 64 * 8;  // elements
-            load_lds16(kr, k_lds + stage * TILE + base, k_src[i]);
-            load_lds16(vr, v_lds + stage * TILE + base, v_src[i]);
+            const int blk = wave * IPW + i;
+            uint32_t ks_off = k_src, vs_off = v_src;
+            if constexpr (LAYOUT == 0) {
+                const int r = lane / CH;
+                const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * KPB + r);
+                ks_off = static_cast<uint32_t>(r) * krow_bytes + gc * 16u;
+                vs_off = static_cast<uint32_t>(r) * vrow_bytes + gc * 16u;
+            }
+            load_lds16(kr, k_lds + stage * TILE + blk * BLK, ks_off, blk * KPB * krow_bytes);
+            load_lds16(vr, v_lds + stage * TILE + blk * BLK, vs_off, blk * KPB * vrow_bytes);
         }
     };
 
@@ -620,10 +639,8 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const int c0 = 2 * ks + hh;
-            const int r0 = l32, r1 = 32 + l32;
-            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(&kl[r0 * ROW + 8 * (c0 ^ kv_swizzle<CH>(r0))]);
-            const u32x4 ka1 = *reinterpret_cast<const u32x4*>(&kl[r1 * ROW + 8 * (c0 ^ kv_swizzle<CH>(r1))]);
+            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(kl + kv_at(l32, 2 * ks + hh));
+            const u32x4 ka1 = *reinterpret_cast<const u32x4*>(kl + kv_at(32 + l32, 2 * ks + hh));
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
                 s[qt][0] = mfma32<T>(ka0, qf[qt][ks], s[qt][0]);
@@ -688,17 +705,27 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
             }
         }
 
-        // ---- O^T += V^T P^T, V^T read transposed from the row-major tile ----
+        // ---- O^T += V^T P^T, V^T read transposed from the key-major planes ----
+        // Lane part of the transposing reads: key 4*hh + li/4 of each 16-key group,
+        // chunk 2*g16 + (li & 3)/2 of each 32-wide d block, 8-byte half li & 1.
+        const uint16_t* vlane = vl + kv_at(4 * hh + (li >> 2), 2 * g16 + ((li & 3) >> 1)) + 4 * (li & 1);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-            const int gc = 4 * db + 2 * g16 + ((li & 3) >> 1);
-            const int half = 4 * (li & 1);
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
-                const int ra = 16 * tt + 4 * hh + (li >> 2);
-                const int rb = ra + 8;
-                const uint2 lo = ds_read_tr16(&vl[ra * ROW + 8 * (gc ^ kv_swizzle<CH>(ra)) + half]);
-                const uint2 hi = ds_read_tr16(&vl[rb * ROW + 8 * (gc ^ kv_swizzle<CH>(rb)) + half]);
+                const uint16_t* va_p;
+                const uint16_t* vb_p;
+                if constexpr (LAYOUT == 0) {
+                    const int key = 16 * tt + 4 * hh + (li >> 2);
+                    const int gc = 4 * db + 2 * g16 + ((li & 3) >> 1);
+                    va_p = vl + kv_at(key, gc) + 4 * (li & 1);
+                    vb_p = vl + kv_at(key + 8, gc) + 4 * (li & 1);
+                } else {
+                    va_p = vlane + kv_at(16 * tt, 4 * db);
+                    vb_p = va_p + kv_at(8, 0);
+                }
+                const uint2 lo = ds_read_tr16(va_p);
+                const uint2 hi = ds_read_tr16(vb_p);
                 const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) o[qt][db] = mfma32<T>(va, pk[qt][tt], o[qt][db]);
@@ -798,14 +825,11 @@ void launch_cfg(FwdParams& prm, bool general, hipStream_t s) {
 }
 
 int tile_override() {
-    static const int v = [] {
-        const char* e = std::getenv("KCR_FA_FWD_TILE");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
+    const char* e = std::getenv("KCR_FA_FWD_TILE");
+    return e ? std::atoi(e) : 0;
 }
 
-template <typename T, int D, int QT, int NW, bool VARLEN>
+template <typename T, int D, int QT, int NW, bool VARLEN, int LAYOUT>
 void launch_v3(FwdParams& prm, hipStream_t s) {
     constexpr int BM = 32 * QT * NW;
     prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
@@ -813,7 +837,7 @@ void launch_v3(FwdParams& prm, hipStream_t s) {
     if (blocks == 0) return;
     if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
     prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
-    flash_fwd_v3_kernel<T, D, QT, NW, VARLEN><<<static_cast<unsigned>(blocks), NW * 64, 0, s>>>(prm);
+    flash_fwd_v3_kernel<T, D, QT, NW, VARLEN, LAYOUT><<<static_cast<unsigned>(blocks), NW * 64, 0, s>>>(prm);
     check_launch("launch flash_fwd");
 }
 
@@ -823,8 +847,8 @@ void launch_d(FwdParams& prm, bool general, hipStream_t s) {
         if (!general) {
             switch (tile_override()) {
                 case 1: break;  // the v2 kernel
-                case 24: return launch_v3<T, D, 2, 4, VARLEN>(prm, s);
-                default: return launch_v3<T, D, 1, 4, VARLEN>(prm, s);
+                case 4: return launch_v3<T, D, 1, 4, VARLEN, 1>(prm, s);
+                default: return launch_v3<T, D, 1, 4, VARLEN, 0>(prm, s);
             }
         }
     }
