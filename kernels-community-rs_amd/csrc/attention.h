@@ -168,5 +168,43 @@ inline bool rows_aligned16(const kcr_tensor* t) {
     return true;
 }
 
+// XOR swizzle of the 16-byte chunks of a row-major LDS tile row with CH = 8 or
+// 16 chunks: the 8 (16) consecutive rows of a ds_read_b128 phase and the 4
+// consecutive rows x 2 chunks of a transposing read land in distinct banks.
+template <int CH>
+__device__ __forceinline__ int kv_swizzle(int row) {
+    return ((row & (CH / 2 - 1)) << 1) | ((row / (CH / 2)) & 1);
+}
+
+using s16x4 = short __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: inside each group of 16 lanes, lane L supplies the
+// address of 4 consecutive 16-bit values; lane i receives value i % 4 of lanes
+// i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4 (a 4 x 16 -> 16 x 4 transpose).
+__device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// Direct HBM -> LDS copy: 16 bytes per lane from `r` at voffset + soffset into
+// LDS at lds_base + 16 * lane (a wave moves 1 KB, lane order).
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, const void* lds_base,
+                                           uint32_t voffset, uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset, soffset, 0, 0);
+}
+
+// Same with 4 bytes per lane (a wave moves 256 bytes).
+__device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, const void* lds_base,
+                                          uint32_t voffset, uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_base), 4, voffset, soffset, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maximum);
+// the direct LDS copies are tracked by vmcnt.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace attn
 }  // namespace kcr

@@ -19,6 +19,8 @@
 //   dQ kernel: the forward's structure with dO added: Q and dO stay in VGPRs,
 //     K/V tiles stream through LDS (K also transposed for dQ^T = K^T dS^T), and
 //     dS^T comes out of the accumulators in the B-operand layout.
+#include <cstdlib>
+
 #include "attention.h"
 
 namespace kcr {
@@ -569,6 +571,418 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
     }
 }
 
+// ---------------------------------------------------------------------------
+// Backward v2 (plain scaled dot product, head size 64 or 128). Tiles are copied
+// HBM -> LDS by direct buffer loads into row-major tiles whose 16-byte chunks are
+// XOR-swizzled per row (kv_swizzle); the row-major reads are ds_read_b128 and
+// every transposed MFMA operand (K^T in dQ, Q^T and dO^T in dK/dV) is read with
+// ds_read_b64_tr_b16 from the same tile, so no transposed copy is ever stored.
+// Two LDS stages, one barrier per tile; 2 waves per SIMD.
+// ---------------------------------------------------------------------------
+
+// Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
+// elements) into a swizzled tile; rows at or past `rows_valid` read as zero.
+// The NW waves move 1 KB blocks of 8 (D = 64) or 4 (D = 128) rows.
+template <int D, int NW, int ROWS>
+__device__ __forceinline__ void copy_rows(const uint16_t* base, int64_t row_stride, int rows_valid,
+                                          uint16_t* tile, int wave, int lane) {
+    constexpr int CH = D / 8;
+    constexpr int RPB = 64 / CH;
+    constexpr int NBLK = ROWS / RPB;
+    static_assert(NBLK % NW == 0, "tile blocks must divide among the waves");
+    constexpr int IPW = NBLK / NW;
+    const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 2u;
+    const uint32_t bytes =
+        rows_valid > 0 ? static_cast<uint32_t>((min(rows_valid, ROWS) - 1) * row_stride + D) * 2u : 0u;
+    const auto r = make_rsrc(base, bytes);
+    const int rr = lane / CH;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        const int blk = wave * IPW + i;
+        const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * RPB + rr);
+        // Whole offset in voffset: the range check that zero-fills rows past the
+        // end covers voffset only.
+        load_lds16(r, tile + blk * 512, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u, 0);
+    }
+}
+
+// Per-lane parts of the swizzled tile addresses. The swizzle of a row depends
+// only on row % (CH) bits that the compile-time parts of the reads (32-row
+// halves, 16-row groups) leave unchanged, so each read is the lane base plus a
+// constant row offset plus 8 * (constant chunk ^ lane chunk key): one XOR.
+template <int D>
+struct TileLane {
+    int rm_base;   // row-major read: row l32
+    int rm_key;    // chunk key: hh ^ swizzle(l32)
+    int tr_base;   // transposed read: row 4hh + li/4, 4-element half li & 1
+    int tr_key_lo; // chunk key of that row: (2 g16 + (li & 3) / 2) ^ swizzle(row)
+    int tr_key_hi; // same for the row 8 further down
+
+    __device__ __forceinline__ TileLane(int lane) {
+        constexpr int CH = D / 8;
+        const int l32 = lane & 31, hh = lane >> 5, g16 = (lane >> 4) & 1, li = lane & 15;
+        rm_base = l32 * D;
+        rm_key = hh ^ kv_swizzle<CH>(l32);
+        const int r0 = 4 * hh + (li >> 2);
+        const int y = 2 * g16 + ((li & 3) >> 1);
+        tr_base = r0 * D + 4 * (li & 1);
+        tr_key_lo = y ^ kv_swizzle<CH>(r0);
+        tr_key_hi = y ^ kv_swizzle<CH>(r0 + 8);
+    }
+    // Hides the keys from loop-invariant hoisting: each read then costs one XOR
+    // instead of a register holding its precomputed address.
+    __device__ __forceinline__ void refresh() {
+        asm volatile("" : "+v"(rm_key), "+v"(tr_key_lo), "+v"(tr_key_hi));
+    }
+    // Row-major 16-byte read of row 32 * half + l32, chunk 2 * ks + hh.
+    __device__ __forceinline__ u32x4 rm(const uint16_t* tile, int half, int ks) const {
+        return *reinterpret_cast<const u32x4*>(tile + rm_base + 32 * half * D + 8 * ((2 * ks) ^ rm_key));
+    }
+    // A operand of X^T = M^T P: element (d, r) = tile[16 tt + r][32 db + d], read
+    // transposed from rows 16tt + 4hh + li/4 and + 8.
+    __device__ __forceinline__ u32x4 tr(const uint16_t* tile, int db, int tt) const {
+        const uint16_t* p = tile + tr_base + 16 * tt * D;
+        const uint2 lo = ds_read_tr16(p + 8 * ((4 * db) ^ tr_key_lo));
+        const uint2 hi = ds_read_tr16(p + 8 * D + 8 * ((4 * db) ^ tr_key_hi));
+        return u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+};
+
+template <typename T, int D, int NW, bool VARLEN>
+__global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dq_v2_kernel(const BwdParams p) {
+    constexpr int BN = 64;
+    constexpr int BM = 32 * NW;
+    constexpr int KS = D / 16;
+    constexpr int DB = D / 32;
+    constexpr int TILE = BN * D;
+
+    __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2 * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2 * TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+    TileLane<D> tl(lane);
+
+    const int per = p.blocks_per_seq;
+    const int qo = blockIdx.x % per;
+    const int bh = blockIdx.x / per;
+    const int b = bh / p.heads;
+    const int head = bh - b * p.heads;
+    const int kvh = head / p.gqa;
+    const int qbi = per - 1 - qo;
+    const SeqBounds sb = seq_bounds<VARLEN>(p, b);
+    if (!sb.ok) return;
+    const int sq = sb.sq, sk = sb.sk;
+    const int row0 = qbi * BM;
+    if (row0 >= sq) return;
+    const int off = sk - sq;
+    const int wl = p.window_left, wr = p.window_right;
+
+    const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head * p.q_h;
+    const uint16_t* dobase = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) + head * p.do_h;
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (VARLEN ? sb.k_off * p.k_s : b * p.k_b) + kvh * p.k_h;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (VARLEN ? sb.k_off * p.v_s : b * p.v_b) + kvh * p.v_h;
+
+    const int my_row = row0 + 32 * wave + l32;
+    u32x4 qf[KS], dof[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 16 * ks + 8 * hh;
+        const bool ok = my_row < sq;
+        qf[ks] = ok ? *reinterpret_cast<const u32x4*>(qbase + my_row * p.q_s + d0) : u32x4{0, 0, 0, 0};
+        dof[ks] = ok ? *reinterpret_cast<const u32x4*>(dobase + my_row * p.do_s + d0) : u32x4{0, 0, 0, 0};
+    }
+    float lse2 = INFINITY, dlt = 0.0f;
+    if (my_row < sq) {
+        lse2 = p.lse[(VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + sb.lse_row0 + my_row] * kLog2e;
+        dlt = p.delta[(VARLEN ? 0 : b * p.delta_b) + head * p.delta_h + sb.delta_row0 + my_row];
+    }
+    const float c = p.scale_log2;
+
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+
+    const int last_row = min(row0 + BM, sq) - 1;
+    int kv_end = sk;
+    if (wr >= 0) kv_end = max(0, min(sk, last_row + 1 + off + wr));
+    int kv_begin = 0;
+    if (wl >= 0) kv_begin = (max(0, min(sk, row0 + off - wl)) / BN) * BN;
+    const int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
+
+    auto copy_tile = [&](int kb, int stage) {
+        copy_rows<D, NW, 64>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE, wave, lane);
+        copy_rows<D, NW, 64>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE, wave, lane);
+    };
+    if (ntiles > 0) {
+        copy_tile(kv_begin, 0);
+        wait_vmem();
+        __syncthreads();
+    }
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int kb = kv_begin + t * BN;
+        tl.refresh();
+        const uint16_t* kl = k_lds + (t & 1) * TILE;
+        const uint16_t* vl = v_lds + (t & 1) * TILE;
+        if (t + 1 < ntiles) copy_tile(kb + BN, (t + 1) & 1);
+
+        f32x16 s[2], dp[2];
+        s[0] = s[1] = dp[0] = dp[1] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+                const u32x4 ka = tl.rm(kl, sub, ks);
+                const u32x4 va = tl.rm(vl, sub, ks);
+                s[sub] = mfma32<T>(ka, qf[ks], s[sub]);
+                dp[sub] = mfma32<T>(va, dof[ks], dp[sub]);
+            }
+        }
+        const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
+                               (wl >= 0 && kb < last_row + off - wl);
+        u32x4 pk[4];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            float dsv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float pr = fast_exp2(__builtin_fmaf(s[sub][r], c, -lse2));
+                if (need_mask) {
+                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    const bool masked = (col >= sk) | (wr >= 0 & col > my_row + off + wr) |
+                                        (wl >= 0 & col < my_row + off - wl);
+                    pr = masked ? 0.0f : pr;
+                }
+                dsv[r] = pr * (dp[sub][r] - dlt);
+            }
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) pk[2 * sub + t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
+            }
+        }
+        // dQ^T += K^T dS^T (K^T read transposed from the key tile)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                acc[db] = mfma32<T>(tl.tr(kl, db, tt), pk[tt], acc[db]);
+            }
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+
+    if (my_row < sq) {
+        uint16_t* dqrow = static_cast<uint16_t*>(p.dq) + (VARLEN ? sb.q_off * p.dq_s : b * p.dq_b) +
+                          head * p.dq_h + my_row * p.dq_s;
+        const float gs = p.grad_scale;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * hh;
+                uint2 a;
+                a.x = pack2<T>(acc[db][4 * g] * gs, acc[db][4 * g + 1] * gs);
+                a.y = pack2<T>(acc[db][4 * g + 2] * gs, acc[db][4 * g + 3] * gs);
+                *reinterpret_cast<uint2*>(dqrow + d) = a;
+            }
+        }
+    }
+}
+
+template <typename T, int D, int NW, bool VARLEN>
+__global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dkv_v2_kernel(const BwdParams p) {
+    // D = 128: the dK and dV accumulators (128 registers) and K (32) leave no
+    // room for V in registers at 2 waves per SIMD, so V is staged once in LDS
+    // and the query tiles shrink to 32 rows to keep two blocks per CU.
+    constexpr bool V_LDS = D > 64;
+    constexpr int BK = 32 * NW;
+    constexpr int BQ = V_LDS ? 32 : 64;
+    constexpr int NQC = BQ / 32;
+    constexpr int KS = D / 16;
+    constexpr int DB = D / 32;
+    constexpr int TILE = BQ * D;
+    static_assert(NW >= 2, "two waves stage the LSE and delta rows");
+
+    __shared__ __attribute__((aligned(1024))) uint16_t q_lds[2 * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t do_lds[2 * TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_lds[V_LDS ? BK * D : 8];
+    // 64 entries per stage: a 4-byte direct copy always writes a whole wave.
+    __shared__ __attribute__((aligned(16))) float lse_lds[2 * 64];
+    __shared__ __attribute__((aligned(16))) float dl_lds[2 * 64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+    TileLane<D> tl(lane);
+
+    const int per = p.blocks_per_seq;
+    const int kbi = blockIdx.x % per;
+    const int bkv = blockIdx.x / per;
+    const int b = bkv / p.kv_heads;
+    const int kvh = bkv - b * p.kv_heads;
+    const SeqBounds sb = seq_bounds<VARLEN>(p, b);
+    if (!sb.ok) return;
+    const int sq = sb.sq, sk = sb.sk;
+    const int key0 = kbi * BK;
+    if (key0 >= sk) return;
+    const int off = sk - sq;
+    const int wl = p.window_left, wr = p.window_right;
+
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (VARLEN ? sb.k_off * p.k_s : b * p.k_b) + kvh * p.k_h;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (VARLEN ? sb.k_off * p.v_s : b * p.v_b) + kvh * p.v_h;
+
+    // This wave's 32 keys: K (and V) rows as B operands of S = Q K^T, dP = dO V^T.
+    const int my_key = key0 + 32 * wave + l32;
+    u32x4 kf[KS];
+    u32x4 vf[V_LDS ? 1 : KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 16 * ks + 8 * hh;
+        const bool ok = my_key < sk;
+        kf[ks] = ok ? *reinterpret_cast<const u32x4*>(kbase + my_key * p.k_s + d0) : u32x4{0, 0, 0, 0};
+        if constexpr (!V_LDS) {
+            vf[ks] = ok ? *reinterpret_cast<const u32x4*>(vbase + my_key * p.v_s + d0) : u32x4{0, 0, 0, 0};
+        }
+    }
+    if constexpr (V_LDS) {
+        copy_rows<D, NW, BK>(vbase + static_cast<int64_t>(key0) * p.v_s, p.v_s, sk - key0, v_lds, wave, lane);
+    }
+    f32x16 dk[DB], dv[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        dk[db] = f32x16{};
+        dv[db] = f32x16{};
+    }
+
+    // Query rows that can see some key of this block.
+    const int key_last = min(key0 + BK, sk) - 1;
+    int q_begin = 0;
+    if (wr >= 0) q_begin = max(0, key0 - off - wr);
+    q_begin = (q_begin / BQ) * BQ;
+    int q_end = sq;
+    if (wl >= 0) q_end = max(0, min(sq, key_last - off + wl + 1));
+    const int nqb = q_begin < q_end ? (q_end - q_begin + BQ - 1) / BQ : 0;
+    const int ntiles = nqb * p.gqa;  // (query head of the group, query tile) pairs, head-major
+    const float c = p.scale_log2;
+
+    auto copy_tile = [&](int t, int stage) {
+        const int j = t / nqb;
+        const int qb = q_begin + (t - j * nqb) * BQ;
+        const int head = kvh * p.gqa + j;
+        const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head * p.q_h;
+        const uint16_t* dobase = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) + head * p.do_h;
+        copy_rows<D, NW, BQ>(qbase + static_cast<int64_t>(qb) * p.q_s, p.q_s, sq - qb, q_lds + stage * TILE, wave, lane);
+        copy_rows<D, NW, BQ>(dobase + static_cast<int64_t>(qb) * p.do_s, p.do_s, sq - qb, do_lds + stage * TILE, wave, lane);
+        // Rows past the sequence read LSE 0 and delta 0; their Q and dO rows are
+        // zero, so they add nothing to dK and dV.
+        const uint32_t rows = static_cast<uint32_t>(max(0, min(sq - qb, BQ)));
+        if (wave == 0) {
+            const float* lse_row = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + sb.lse_row0 + qb;
+            load_lds4(make_rsrc(lse_row, rows * 4u), lse_lds + stage * 64, lane * 4u, 0);
+        } else if (wave == 1) {
+            const float* dl_row = p.delta + (VARLEN ? 0 : b * p.delta_b) + head * p.delta_h + sb.delta_row0 + qb;
+            load_lds4(make_rsrc(dl_row, rows * 4u), dl_lds + stage * 64, lane * 4u, 0);
+        }
+    };
+    if (ntiles > 0) copy_tile(0, 0);
+    wait_vmem();
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        tl.refresh();
+        const int stage = t & 1;
+        const int qb = q_begin + (t % nqb) * BQ;
+        const uint16_t* ql = q_lds + stage * TILE;
+        const uint16_t* dl = do_lds + stage * TILE;
+        const float* lsl = lse_lds + stage * 64;
+        const float* dll = dl_lds + stage * 64;
+        if (t + 1 < ntiles) copy_tile(t + 1, stage ^ 1);
+
+        const bool need_mask = (key0 + BK > sk) || (wr >= 0 && key0 + BK - 1 > qb + off + wr) ||
+                               (wl >= 0 && key0 < qb + BQ - 1 + off - wl);
+#pragma unroll
+        for (int qc = 0; qc < NQC; ++qc) {
+            f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                s = mfma32<T>(tl.rm(ql, qc, ks), kf[ks], s);
+                if constexpr (V_LDS) {
+                    dp = mfma32<T>(tl.rm(dl, qc, ks), tl.rm(v_lds, wave, ks), dp);
+                } else {
+                    dp = mfma32<T>(tl.rm(dl, qc, ks), vf[ks], dp);
+                }
+            }
+            u32x4 pP[2], pS[2];
+            float pv[16], dsv[16];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int qloc = 32 * qc + 8 * g + 4 * hh;
+                const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
+                const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                    if (need_mask) {
+                        const int row = qb + qloc + e;
+                        const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
+                                            (wl >= 0 & my_key < row + off - wl);
+                        pr = masked ? 0.0f : pr;
+                    }
+                    pv[r] = pr;
+                    dsv[r] = pr * (dp[r] - dv4[e]);
+                }
+            }
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    pP[t2][w] = pack2<T>(pv[8 * t2 + 2 * w], pv[8 * t2 + 2 * w + 1]);
+                    pS[t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
+                }
+            }
+            // dV^T += dO^T P and dK^T += Q^T dS (transposed reads of the query tiles)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2) {
+                    const int tt = 2 * qc + t2;
+                    dv[db] = mfma32<T>(tl.tr(dl, db, tt), pP[t2], dv[db]);
+                    dk[db] = mfma32<T>(tl.tr(ql, db, tt), pS[t2], dk[db]);
+                }
+            }
+        }
+        wait_vmem();
+        __syncthreads();
+    }
+
+    if (my_key < sk) {
+        uint16_t* dkrow = static_cast<uint16_t*>(p.dk) + (VARLEN ? sb.k_off * p.dk_s : b * p.dk_b) +
+                          kvh * p.dk_h + my_key * p.dk_s;
+        uint16_t* dvrow = static_cast<uint16_t*>(p.dv) + (VARLEN ? sb.k_off * p.dv_s : b * p.dv_b) +
+                          kvh * p.dv_h + my_key * p.dv_s;
+        const float gs = p.grad_scale;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * hh;
+                uint2 a, cc;
+                a.x = pack2<T>(dk[db][4 * g] * gs, dk[db][4 * g + 1] * gs);
+                a.y = pack2<T>(dk[db][4 * g + 2] * gs, dk[db][4 * g + 3] * gs);
+                cc.x = pack2<T>(dv[db][4 * g], dv[db][4 * g + 1]);
+                cc.y = pack2<T>(dv[db][4 * g + 2], dv[db][4 * g + 3]);
+                *reinterpret_cast<uint2*>(dkrow + d) = a;
+                *reinterpret_cast<uint2*>(dvrow + d) = cc;
+            }
+        }
+    }
+}
+
 __global__ void zero_u16_kernel(uint16_t* x, int64_t n) {
     for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += gridDim.x * 256ll) x[i] = 0;
 }
@@ -599,8 +1013,40 @@ void zero_f32(float* x, int64_t n, hipStream_t s) {
     check_launch("zero delta");
 }
 
+int bwd_override() {
+    const char* e = std::getenv("KCR_FA_BWD_V1");
+    return e ? std::atoi(e) : 0;
+}
+
 template <typename T, int D, bool VARLEN, bool GEN>
 void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
+    if constexpr (!GEN && (D == 64 || D == 128)) {
+        // The tiled kernels need the full bucket width and 32-bit tile offsets.
+        constexpr int64_t kMaxStride = int64_t{1} << 23;
+        const bool fits = prm.head_dim == D && prm.q_s <= kMaxStride && prm.k_s <= kMaxStride &&
+                          prm.v_s <= kMaxStride && prm.do_s <= kMaxStride;
+        if (fits && !bwd_override()) {
+            if (want_kv) {
+                constexpr int BK = 32 * kDkvWaves;
+                prm.blocks_per_seq = (prm.seqlen_k + BK - 1) / BK;
+                const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.kv_heads;
+                if (blocks > 0) {
+                    flash_bwd_dkv_v2_kernel<T, D, kDkvWaves, VARLEN><<<static_cast<unsigned>(blocks), kDkvWaves * 64, 0, s>>>(prm);
+                    check_launch("launch flash_bwd_dkv");
+                }
+            }
+            if (want_q) {
+                constexpr int BM = 32 * kDqWaves;
+                prm.blocks_per_seq = (prm.seqlen_q + BM - 1) / BM;
+                const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.heads;
+                if (blocks > 0) {
+                    flash_bwd_dq_v2_kernel<T, D, kDqWaves, VARLEN><<<static_cast<unsigned>(blocks), kDqWaves * 64, 0, s>>>(prm);
+                    check_launch("launch flash_bwd_dq");
+                }
+            }
+            return;
+        }
+    }
     if (want_kv) {
         constexpr int BK = 32 * kDkvWaves;
         prm.blocks_per_seq = (prm.seqlen_k + BK - 1) / BK;

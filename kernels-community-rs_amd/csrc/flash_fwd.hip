@@ -438,30 +438,6 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // (the padding puts neighbouring blocks 16 banks apart).
 // Two LDS stages; the next tile's copy is in flight during the current tile.
 // ---------------------------------------------------------------------------
-using s16x4 = short __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
-    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(p));
-    return __builtin_bit_cast(uint2, v);
-}
-
-// 16 bytes per lane from `r` at byte `voffset` into LDS at lds_base + 16 * lane.
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, const uint16_t* lds_base,
-                                           uint32_t voffset, uint32_t soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset, soffset, 0, 0);
-}
-
-// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maximum).
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-template <int CH>
-__device__ __forceinline__ int kv_swizzle(int row) {
-    // XOR swizzle of the 16-byte chunks of a row-major tile row (CH = 8 or 16).
-    return ((row & (CH / 2 - 1)) << 1) | ((row / (CH / 2)) & 1);
-}
-
 // LAYOUT 1: 4-key blocks (above). LAYOUT 0: row-major rows with the chunks of
 // each row XOR-swizzled by kv_swizzle (one 1 KB copy = 4 rows; addresses of the
 // reads need per-lane XOR arithmetic).
@@ -609,8 +585,10 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
                 ks_off = static_cast<uint32_t>(r) * krow_bytes + gc * 16u;
                 vs_off = static_cast<uint32_t>(r) * vrow_bytes + gc * 16u;
             }
-            load_lds16(kr, k_lds + stage * TILE + blk * BLK, ks_off, blk * KPB * krow_bytes);
-            load_lds16(vr, v_lds + stage * TILE + blk * BLK, vs_off, blk * KPB * vrow_bytes);
+            // The whole offset goes in voffset: the hardware range check that
+            // zero-fills rows past the sequence end covers voffset only.
+            load_lds16(kr, k_lds + stage * TILE + blk * BLK, ks_off + blk * KPB * krow_bytes, 0);
+            load_lds16(vr, v_lds + stage * TILE + blk * BLK, vs_off + blk * KPB * vrow_bytes, 0);
         }
     };
 
