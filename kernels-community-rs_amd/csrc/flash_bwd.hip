@@ -663,12 +663,18 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dq_v2_kernel(const BwdPa
     const int l32 = lane & 31, hh = lane >> 5;
     TileLane<D> tl(lane);
 
+    // Tile-major order, longest causal tiles first across the whole grid; the
+    // query heads of one KV head share blockIdx % (B * Hk), hence one XCD when
+    // B * Hk is a multiple of 8 (K/V tiles stay in that XCD's L2).
     const int per = p.blocks_per_seq;
-    const int qo = blockIdx.x % per;
-    const int bh = blockIdx.x / per;
-    const int b = bh / p.heads;
-    const int head = bh - b * p.heads;
-    const int kvh = head / p.gqa;
+    const int nbh = p.batch * p.heads;
+    const int nbkv = p.batch * p.kv_heads;
+    const int qo = blockIdx.x / nbh;
+    const int idx = blockIdx.x - qo * nbh;
+    const int g = idx % nbkv;
+    const int b = g / p.kv_heads;
+    const int kvh = g - b * p.kv_heads;
+    const int head = kvh * p.gqa + idx / nbkv;
     const int qbi = per - 1 - qo;
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
     if (!sb.ok) return;
@@ -817,9 +823,11 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dkv_v2_kernel(const BwdP
     const int l32 = lane & 31, hh = lane >> 5;
     TileLane<D> tl(lane);
 
-    const int per = p.blocks_per_seq;
-    const int kbi = blockIdx.x % per;
-    const int bkv = blockIdx.x / per;
+    // Tile-major order: the key tiles that see the most causal queries start
+    // first across the whole grid; one (batch, KV head) keeps one XCD.
+    const int nbkv = p.batch * p.kv_heads;
+    const int kbi = blockIdx.x / nbkv;
+    const int bkv = blockIdx.x - kbi * nbkv;
     const int b = bkv / p.kv_heads;
     const int kvh = bkv - b * p.kv_heads;
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
