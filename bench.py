@@ -135,7 +135,7 @@ def _wl_fa_bwd(causal):
             ops.bwd_all(q, k, v, dout, lse, delta, *args)
 
         flops = 2.5 * 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
-        return dict(run=run, work=flops, bound="mfma", kernel="flash_bwd",
+        return dict(run=run, work=flops, bound="mfma", kernel="flash_bwd_dkv",
                     config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
                             "dtype": "bf16"},
                     cpu=None)
@@ -180,12 +180,27 @@ def _wl_fa_varlen(kind):
                                         0.0, 0.0, None, mx, mx, False)
 
             work = 2.5 * fwd_flops
-        return dict(run=run, work=work, bound="mfma", kernel=f"flash_varlen_{kind}",
+        return dict(run=run, work=work, bound="mfma", kernel="flash_fwd" if kind == "fwd" else "flash_bwd_dkv",
                     config={"seqs": len(lens), "sum_L": total, "sum_L2": sum_sq, "Hq": hq,
                             "Hkv": hkv, "D": d, "causal": True, "dtype": "bf16"},
                     cpu=None)
 
     return make
+
+
+def wl_hbm_copy():
+    """Plain device copy of the activation input size (939,524,096 B read and
+    written): the known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE
+    counters, and the practical HBM ceiling beside the 8 TB/s peak."""
+    g = _gen(2)
+    x = torch.randn(16384, 28672, generator=g).bfloat16().cuda()
+    y = torch.empty_like(x)
+
+    def run():
+        y.copy_(x)
+
+    return dict(run=run, work=2 * x.numel() * 2, bound="hbm", kernel="elementwise_kernel",
+                config={"x": list(x.shape), "dtype": "bf16"}, cpu=None)
 
 
 WORKLOADS = {
@@ -199,7 +214,9 @@ WORKLOADS = {
     "silu_and_mul": _wl_gated("silu_and_mul"),
     "gelu_and_mul": _wl_gated("gelu_and_mul"),
     "gelu_tanh_and_mul": _wl_gated("gelu_tanh_and_mul"),
+    "hbm_copy": wl_hbm_copy,
 }
+DEFAULT_ORDER = [n for n in WORKLOADS if n != "hbm_copy"]
 
 # --------------------------------------------------------------------------
 # CPU baselines: the oracle (the tests' formulas restated in numpy), timed on a
@@ -284,7 +301,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--headline", default="fa_fwd_causal")
     ap.add_argument("--only", default=None, help="comma-separated workloads (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -297,7 +314,7 @@ def main():
         print("bench.py is single-GPU; launch it without torch.distributed.run", file=sys.stderr)
         sys.exit(2)
 
-    names = args.only.split(",") if args.only else list(WORKLOADS)
+    names = args.only.split(",") if args.only else list(DEFAULT_ORDER)
     if args.headline not in names:
         names.insert(0, args.headline)
     results = {}
@@ -331,7 +348,8 @@ def main():
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get(wl["kernel"])
+        entry = json.loads(tfile.read_text()).get(args.headline)
+        traffic = entry.get("hbm_bytes_per_launch") if entry else None
     line = {
         "metric": METRIC,
         "value": round(achieved, 2),

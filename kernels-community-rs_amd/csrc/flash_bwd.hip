@@ -649,7 +649,7 @@ struct TileLane {
 };
 
 template <typename T, int D, int NW, bool VARLEN>
-__global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dq_v2_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {
     constexpr int BN = 64;
     constexpr int BM = 32 * NW;
     constexpr int KS = D / 16;
@@ -675,10 +675,12 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dq_v2_kernel(const BwdPa
     const int b = g / p.kv_heads;
     const int kvh = g - b * p.kv_heads;
     const int head = kvh * p.gqa + idx / nbkv;
-    const int qbi = per - 1 - qo;
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
+    // Counted from the end of this sequence (varlen sequences end at different tiles).
+    const int qbi = (VARLEN ? (sq + BM - 1) / BM : per) - 1 - qo;
+    if (qbi < 0) return;
     const int row0 = qbi * BM;
     if (row0 >= sq) return;
     const int off = sk - sq;
@@ -799,7 +801,7 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dq_v2_kernel(const BwdPa
 }
 
 template <typename T, int D, int NW, bool VARLEN>
-__global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dkv_v2_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const BwdParams p) {
     // D = 128: the dK and dV accumulators (128 registers) and K (32) leave no
     // room for V in registers at 2 waves per SIMD, so V is staged once in LDS
     // and the query tiles shrink to 32 rows to keep two blocks per CU.
@@ -872,12 +874,18 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dkv_v2_kernel(const BwdP
     int q_end = sq;
     if (wl >= 0) q_end = max(0, min(sq, key_last - off + wl + 1));
     const int nqb = q_begin < q_end ? (q_end - q_begin + BQ - 1) / BQ : 0;
-    const int ntiles = nqb * p.gqa;  // (query head of the group, query tile) pairs, head-major
+    // (query tile, query head of the group) pairs, last query tile first: the
+    // key blocks of one (batch, KV head) run on one XCD and all end at the last
+    // query tile, so walking the tiles downward keeps them reading the same
+    // Q / dO tiles at the same time (shared through L2).
+    const int gqa = p.gqa;
+    const int ntiles = nqb * gqa;
     const float c = p.scale_log2;
 
+    auto tile_row0 = [&](int t) { return q_begin + (nqb - 1 - t / gqa) * BQ; };
     auto copy_tile = [&](int t, int stage) {
-        const int j = t / nqb;
-        const int qb = q_begin + (t - j * nqb) * BQ;
+        const int j = t % gqa;
+        const int qb = tile_row0(t);
         const int head = kvh * p.gqa + j;
         const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head * p.q_h;
         const uint16_t* dobase = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) + head * p.do_h;
@@ -901,7 +909,7 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_bwd_dkv_v2_kernel(const BwdP
     for (int t = 0; t < ntiles; ++t) {
         tl.refresh();
         const int stage = t & 1;
-        const int qb = q_begin + (t % nqb) * BQ;
+        const int qb = tile_row0(t);
         const uint16_t* ql = q_lds + stage * TILE;
         const uint16_t* dl = do_lds + stage * TILE;
         const float* lsl = lse_lds + stage * 64;
@@ -1021,6 +1029,28 @@ void zero_f32(float* x, int64_t n, hipStream_t s) {
     check_launch("zero delta");
 }
 
+template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES>
+void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
+    if (want_kv) {
+        constexpr int BK = 32 * DKV_WAVES;
+        prm.blocks_per_seq = (prm.seqlen_k + BK - 1) / BK;
+        const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.kv_heads;
+        if (blocks > 0) {
+            flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN><<<static_cast<unsigned>(blocks), DKV_WAVES * 64, 0, s>>>(prm);
+            check_launch("launch flash_bwd_dkv");
+        }
+    }
+    if (want_q) {
+        constexpr int BM = 32 * DQ_WAVES;
+        prm.blocks_per_seq = (prm.seqlen_q + BM - 1) / BM;
+        const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.heads;
+        if (blocks > 0) {
+            flash_bwd_dq_v2_kernel<T, D, DQ_WAVES, VARLEN><<<static_cast<unsigned>(blocks), DQ_WAVES * 64, 0, s>>>(prm);
+            check_launch("launch flash_bwd_dq");
+        }
+    }
+}
+
 int bwd_override() {
     const char* e = std::getenv("KCR_FA_BWD_V1");
     return e ? std::atoi(e) : 0;
@@ -1034,23 +1064,16 @@ void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
         const bool fits = prm.head_dim == D && prm.q_s <= kMaxStride && prm.k_s <= kMaxStride &&
                           prm.v_s <= kMaxStride && prm.do_s <= kMaxStride;
         if (fits && !bwd_override()) {
-            if (want_kv) {
-                constexpr int BK = 32 * kDkvWaves;
-                prm.blocks_per_seq = (prm.seqlen_k + BK - 1) / BK;
-                const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.kv_heads;
-                if (blocks > 0) {
-                    flash_bwd_dkv_v2_kernel<T, D, kDkvWaves, VARLEN><<<static_cast<unsigned>(blocks), kDkvWaves * 64, 0, s>>>(prm);
-                    check_launch("launch flash_bwd_dkv");
-                }
-            }
-            if (want_q) {
-                constexpr int BM = 32 * kDqWaves;
-                prm.blocks_per_seq = (prm.seqlen_q + BM - 1) / BM;
-                const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.heads;
-                if (blocks > 0) {
-                    flash_bwd_dq_v2_kernel<T, D, kDqWaves, VARLEN><<<static_cast<unsigned>(blocks), kDqWaves * 64, 0, s>>>(prm);
-                    check_launch("launch flash_bwd_dq");
-                }
+            const char* w = std::getenv("KCR_FA_BWD_WAVES");
+            const int waves = w ? std::atoi(w) : 4;
+            if (waves == 8) {
+                launch_bwd_v2<T, D, VARLEN, 8, 8>(prm, want_q, want_kv, s);
+            } else if (waves == 48) {
+                launch_bwd_v2<T, D, VARLEN, 4, 8>(prm, want_q, want_kv, s);
+            } else if (waves == 84) {
+                launch_bwd_v2<T, D, VARLEN, 8, 4>(prm, want_q, want_kv, s);
+            } else {
+                launch_bwd_v2<T, D, VARLEN, 4, 4>(prm, want_q, want_kv, s);
             }
             return;
         }

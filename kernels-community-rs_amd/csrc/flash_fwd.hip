@@ -96,7 +96,9 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     const int b = bh / p.heads;
     const int head = bh - b * p.heads;
     const int kvh = head / p.gqa;
-    const int qb = p.q_blocks - 1 - qo;  // longest causal tiles first
+    // Longest causal tiles first: block qo takes the qo-th query tile counted
+    // from the end of its own sequence (varlen sequences end at different tiles).
+    int qb = p.q_blocks - 1 - qo;
 
     int64_t q_off = 0, k_off = 0;
     int sq = p.seqlen_q, sk = p.seqlen_k;
@@ -118,6 +120,8 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
         q_off = static_cast<int64_t>(qs);
         k_off = static_cast<int64_t>(ks + pad);
         lse_row0 = qs;
+        qb = (sq + BM - 1) / BM - 1 - qo;
+        if (qb < 0) return;
     }
     const int row0 = qb * BM;
     if (row0 >= sq) return;
@@ -488,7 +492,9 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
     const int b = bh / p.heads;
     const int head = bh - b * p.heads;
     const int kvh = head / p.gqa;
-    const int qb = p.q_blocks - 1 - qo;
+    // Longest causal tiles first: block qo takes the qo-th query tile counted
+    // from the end of its own sequence (varlen sequences end at different tiles).
+    int qb = p.q_blocks - 1 - qo;
 
     int64_t q_off = 0, k_off = 0;
     int sq = p.seqlen_q, sk = p.seqlen_k;
@@ -509,6 +515,8 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
         q_off = static_cast<int64_t>(qs);
         k_off = static_cast<int64_t>(ks + pad);
         lse_row0 = qs;
+        qb = (sq + BM - 1) / BM - 1 - qo;
+        if (qb < 0) return;
     }
     const int row0 = qb * BM;
     if (row0 >= sq) return;
