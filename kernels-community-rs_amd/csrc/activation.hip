@@ -34,12 +34,68 @@ __device__ __forceinline__ float rnd(float v) {
     return Elem<T>::round(v);
 }
 
-// act(x) for an element already widened to f32; the result is rounded to T.
-// `threshold` is only used by FATReLU.
+// exp(x) for x in [-150, 80]: exp2 of the product x * log2(e) split into a
+// rounded head and its exact residual (the head via one multiply, the residual
+// via two FMAs against the two-float log2(e)), then one first-order correction
+// e * (1 + residual * ln 2). Relative error about 1 ulp of f32 (v_exp_f32's own).
+__device__ __forceinline__ float exp_split(float x) {
+    constexpr float kLog2eHi = 1.44269502162933349609375f;  // float(log2 e)
+    constexpr float kLog2eLo = 1.9259629911266175e-8f;      // log2 e - kLog2eHi
+    constexpr float kLn2f = 0.693147180559945309f;
+    const float h = x * kLog2eHi;
+    const float lo = __builtin_fmaf(x, kLog2eLo, __builtin_fmaf(x, kLog2eHi, -h));
+    const float e2 = __builtin_amdgcn_exp2f(h);
+    return __builtin_fmaf(e2 * lo, kLn2f, e2);
+}
+
+// f / (1 + exp(-z)) for z > -80 (so 1 + exp(-z) < 2^116 and its reciprocal is
+// a normal float) and finite f below 2^64: hardware reciprocal plus one Newton-Raphson correction of the
+// quotient, within about 1 ulp of the IEEE quotient. Used for 16-bit element
+// types, whose results are rounded to 8 or 11 significant bits afterwards.
+__device__ __forceinline__ float div_one_plus_exp_neg(float f, float z) {
+    const float d = 1.0f + exp_split(fmaxf(-z, -150.0f));
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q0 = f * r;
+    return __builtin_fmaf(__builtin_fmaf(-d, q0, f), r, q0);
+}
+
+// tanh(u) = sign(u) (1 - s), s = 2e / (1 + e), e = exp(-2|u|) in (0, 1], with
+// e = exp2(-2|u| log2 e) and the hardware reciprocal. The errors of e and s
+// (a few f32 ulp, relative) reach 1 - s only as s times that, below half an ulp
+// of 1 wherever s is small (|u| large, where 1 + tanh(u) cancels), so the
+// reference's rounding of tanh and of 1 + tanh is reproduced there. Infinite u
+// gives +-1; NaN u gives +-1 and the callers' products with the NaN input stay
+// NaN.
+__device__ __forceinline__ float tanh_lite(float u) {
+    constexpr float kNeg2Log2e = -2.0f * 1.44269502162933349609375f;
+    const float e = __builtin_amdgcn_exp2f(fmaxf(fabsf(u) * kNeg2Log2e, -300.0f));
+    const float s = e * __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, e, 0.5f));  // 2e / (1 + e)
+    return copysignf(1.0f - s, u);
+}
+
+// Whether the split-exp forms may stand in for the libm expression: 16-bit
+// element types only (their results keep 8 or 11 significant bits).
 template <typename T, int A>
+constexpr bool has_fast_form() {
+    return sizeof(typename Elem<T>::storage) == 2 && (A == ACT_SILU || A == ACT_GELU_TANH);
+}
+
+// Inputs the fast SiLU form covers: the split exp needs -f < 80 (no overflow of
+// 1 + exp(-f), normal reciprocal), the Newton step a finite f below 2^64. The
+// tails (and NaN) keep the reference expression.
+template <int A>
+__device__ __forceinline__ bool fast_form_covers(float f) {
+    if constexpr (A == ACT_SILU) return f > -80.0f && f < 0x1p64f;
+    return true;
+}
+
+template <typename T, int A, bool FAST = false>
 __device__ __forceinline__ float apply_act(float f, float threshold) {
+    constexpr bool kFast = FAST && has_fast_form<T, A>();
     if constexpr (A == ACT_SILU) {
-        // activation.rs:42-46: f / (1 + exp(-f))
+        // activation.rs:42-46: f / (1 + exp(-f)); the fast form is the split exp
+        // and a refined reciprocal (callers check fast_form_covers first).
+        if constexpr (kFast) return rnd<T>(div_one_plus_exp_neg(f, f));
         return rnd<T>(f / (1.0f + expf(-f)));
     } else if constexpr (A == ACT_GELU) {
         // activation.rs:53-58: f * 0.5 * (1 + erf(f / sqrt(2)))
@@ -52,6 +108,9 @@ __device__ __forceinline__ float apply_act(float f, float threshold) {
         const float kappa = 0.044715f;
         const float x_cube = f * f * f;
         const float inner = beta * __builtin_fmaf(kappa, x_cube, f);
+        // 16-bit types: tanh from one exp2 and one reciprocal (tanh_lite), then
+        // the reference's own 1 + tanh(u) and products.
+        if constexpr (kFast) return rnd<T>(0.5f * f * (1.0f + tanh_lite(inner)));
         return rnd<T>(0.5f * f * (1.0f + tanhf(inner)));
     } else if constexpr (A == ACT_GELU_NEW) {
         // activation.rs:79-90, every intermediate in T.
@@ -74,12 +133,12 @@ __device__ __forceinline__ float apply_act(float f, float threshold) {
     }
 }
 
-template <typename T, int A, bool ACT_FIRST>
+template <typename T, int A, bool ACT_FIRST, bool FAST = false>
 __device__ __forceinline__ float gated(float x, float y, float threshold) {
     if constexpr (ACT_FIRST) {
-        return apply_act<T, A>(x, threshold) * y;
+        return apply_act<T, A, FAST>(x, threshold) * y;
     } else {
-        return x * apply_act<T, A>(y, threshold);
+        return x * apply_act<T, A, FAST>(y, threshold);
     }
 }
 
@@ -157,8 +216,18 @@ __global__ void __launch_bounds__(kThreads) act_and_mul_vec(u32x4* __restrict__ 
             float x[VEC], y[VEC], r[VEC];
             widen<T>(xs[u], x);
             widen<T>(ys[u], y);
+            // One branch per vector: the fast form when it covers every element
+            // of this lane's vector (always, for ordinary data).
+            bool fast = has_fast_form<T, A>();
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) r[e] = gated<T, A, ACT_FIRST>(x[e], y[e], threshold);
+            for (int e = 0; e < VEC; ++e) fast = fast && fast_form_covers<A>(ACT_FIRST ? x[e] : y[e]);
+            if (fast) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) r[e] = gated<T, A, ACT_FIRST, true>(x[e], y[e], threshold);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) r[e] = gated<T, A, ACT_FIRST>(x[e], y[e], threshold);
+            }
             __builtin_nontemporal_store(narrow<T>(r), out + oidx[u]);
         }
     }
