@@ -77,7 +77,10 @@ __device__ __forceinline__ float tanh_lite(float u) {
 // element types only (their results keep 8 or 11 significant bits).
 template <typename T, int A>
 constexpr bool has_fast_form() {
-    return sizeof(typename Elem<T>::storage) == 2 && (A == ACT_SILU || A == ACT_GELU_TANH);
+    // gelu_tanh: bf16 only; f16's 11-bit results near the cancellation of
+    // 1 + tanh(u) resolve the few-ulp error of the exp2 / reciprocal form.
+    return (sizeof(typename Elem<T>::storage) == 2 && A == ACT_SILU) ||
+           (std::is_same<T, bf16_t>::value && A == ACT_GELU_TANH);
 }
 
 // Inputs the fast SiLU form covers: the split exp needs -f < 80 (no overflow of
@@ -108,7 +111,7 @@ __device__ __forceinline__ float apply_act(float f, float threshold) {
         const float kappa = 0.044715f;
         const float x_cube = f * f * f;
         const float inner = beta * __builtin_fmaf(kappa, x_cube, f);
-        // 16-bit types: tanh from one exp2 and one reciprocal (tanh_lite), then
+        // bf16: tanh from one exp2 and one reciprocal (tanh_lite), then
         // the reference's own 1 + tanh(u) and products.
         if constexpr (kFast) return rnd<T>(0.5f * f * (1.0f + tanh_lite(inner)));
         return rnd<T>(0.5f * f * (1.0f + tanhf(inner)));

@@ -168,12 +168,24 @@ inline bool rows_aligned16(const kcr_tensor* t) {
     return true;
 }
 
-// XOR swizzle of the 16-byte chunks of a row-major LDS tile row with CH = 8 or
-// 16 chunks: the 8 (16) consecutive rows of a ds_read_b128 phase and the 4
-// consecutive rows x 2 chunks of a transposing read land in distinct banks.
+// XOR swizzle of the 16-byte chunks of a row-major LDS tile row with CH = 16
+// (D = 128, 256-byte rows) or CH = 8 (D = 64, 128-byte rows): the chunk of
+// row r is stored at chunk ^ kv_swizzle(r). Chosen for gfx950's 256-byte LDS
+// bank window (measured on the device):
+//   - ds_read_b128 serves 16 lanes per pass; they read 16 consecutive rows at one
+//     logical chunk, and the swizzle maps those rows to 16 distinct 16-byte slots;
+//   - ds_read_b64_tr_b16 serves 32 lanes per pass; they read 4 rows x 4 chunks,
+//     and the swizzle gives each of the 4 rows its own 64-byte quarter.
+// The value depends on row bits 0..3 only, so row offsets that are multiples of
+// 16 keep it.
 template <int CH>
 __device__ __forceinline__ int kv_swizzle(int row) {
-    return ((row & (CH / 2 - 1)) << 1) | ((row / (CH / 2)) & 1);
+    static_assert(CH == 8 || CH == 16, "16-byte chunks per row: 8 or 16");
+    if constexpr (CH == 16) {
+        return 4 * (row & 3) + ((row >> 2) & 3);
+    } else {
+        return 4 * ((row >> 1) & 1) + ((row >> 2) & 1);
+    }
 }
 
 using s16x4 = short __attribute__((ext_vector_type(4)));
@@ -205,6 +217,74 @@ __device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, const void* 
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maximum);
 // the direct LDS copies are tracked by vmcnt.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
+// elements) into a swizzled tile; rows at or past `rows_valid` read as zero.
+// The NW waves move 1 KB blocks of 8 (D = 64) or 4 (D = 128) rows.
+template <int D, int NW, int ROWS>
+__device__ __forceinline__ void copy_rows(const uint16_t* base, int64_t row_stride, int rows_valid,
+                                          uint16_t* tile, int wave, int lane) {
+    constexpr int CH = D / 8;
+    constexpr int RPB = 64 / CH;
+    constexpr int NBLK = ROWS / RPB;
+    static_assert(NBLK % NW == 0, "tile blocks must divide among the waves");
+    constexpr int IPW = NBLK / NW;
+    const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 2u;
+    const uint32_t bytes =
+        rows_valid > 0 ? static_cast<uint32_t>((min(rows_valid, ROWS) - 1) * row_stride + D) * 2u : 0u;
+    const auto r = make_rsrc(base, bytes);
+    const int rr = lane / CH;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        const int blk = wave * IPW + i;
+        const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * RPB + rr);
+        // Whole offset in voffset: the range check that zero-fills rows past the
+        // end covers voffset only.
+        load_lds16(r, tile + blk * 512, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u, 0);
+    }
+}
+
+// Per-lane parts of the swizzled tile addresses. The swizzle of a row depends
+// only on row bits that the compile-time parts of the reads (32-row halves,
+// 16-row groups) leave unchanged, so each read is the lane base plus a
+// constant row offset plus 8 * (constant chunk ^ lane chunk key): one XOR.
+template <int D>
+struct TileLane {
+    int rm_base;   // row-major read: row l32
+    int rm_key;    // chunk key: hh ^ swizzle(l32)
+    int tr_base;   // transposed read: row 4hh + li/4, 4-element half li & 1
+    int tr_key_lo; // chunk key of that row: (2 g16 + (li & 3) / 2) ^ swizzle(row)
+    int tr_key_hi; // same for the row 8 further down
+
+    __device__ __forceinline__ TileLane(int lane) {
+        constexpr int CH = D / 8;
+        const int l32 = lane & 31, hh = lane >> 5, g16 = (lane >> 4) & 1, li = lane & 15;
+        rm_base = l32 * D;
+        rm_key = hh ^ kv_swizzle<CH>(l32);
+        const int r0 = 4 * hh + (li >> 2);
+        const int y = 2 * g16 + ((li & 3) >> 1);
+        tr_base = r0 * D + 4 * (li & 1);
+        tr_key_lo = y ^ kv_swizzle<CH>(r0);
+        tr_key_hi = y ^ kv_swizzle<CH>(r0 + 8);
+    }
+    // Hides the keys from loop-invariant hoisting: each read then costs one XOR
+    // instead of a register holding its precomputed address.
+    __device__ __forceinline__ void refresh() {
+        asm volatile("" : "+v"(rm_key), "+v"(tr_key_lo), "+v"(tr_key_hi));
+    }
+    // Row-major 16-byte read of row 32 * half + l32, chunk 2 * ks + hh.
+    __device__ __forceinline__ u32x4 rm(const uint16_t* tile, int half, int ks) const {
+        return *reinterpret_cast<const u32x4*>(tile + rm_base + 32 * half * D + 8 * ((2 * ks) ^ rm_key));
+    }
+    // A operand of X^T = M^T P: element (d, r) = tile[16 tt + r][32 db + d], read
+    // transposed from rows 16tt + 4hh + li/4 and + 8.
+    __device__ __forceinline__ u32x4 tr(const uint16_t* tile, int db, int tt) const {
+        const uint16_t* p = tile + tr_base + 16 * tt * D;
+        const uint2 lo = ds_read_tr16(p + 8 * ((4 * db) ^ tr_key_lo));
+        const uint2 hi = ds_read_tr16(p + 8 * D + 8 * ((4 * db) ^ tr_key_hi));
+        return u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+};
 
 }  // namespace attn
 }  // namespace kcr

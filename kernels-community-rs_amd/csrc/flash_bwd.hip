@@ -19,8 +19,6 @@
 //   dQ kernel: the forward's structure with dO added: Q and dO stay in VGPRs,
 //     K/V tiles stream through LDS (K also transposed for dQ^T = K^T dS^T), and
 //     dS^T comes out of the accumulators in the B-operand layout.
-#include <cstdlib>
-
 #include "attention.h"
 
 namespace kcr {
@@ -580,74 +578,6 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 // Two LDS stages, one barrier per tile; 2 waves per SIMD.
 // ---------------------------------------------------------------------------
 
-// Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
-// elements) into a swizzled tile; rows at or past `rows_valid` read as zero.
-// The NW waves move 1 KB blocks of 8 (D = 64) or 4 (D = 128) rows.
-template <int D, int NW, int ROWS>
-__device__ __forceinline__ void copy_rows(const uint16_t* base, int64_t row_stride, int rows_valid,
-                                          uint16_t* tile, int wave, int lane) {
-    constexpr int CH = D / 8;
-    constexpr int RPB = 64 / CH;
-    constexpr int NBLK = ROWS / RPB;
-    static_assert(NBLK % NW == 0, "tile blocks must divide among the waves");
-    constexpr int IPW = NBLK / NW;
-    const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 2u;
-    const uint32_t bytes =
-        rows_valid > 0 ? static_cast<uint32_t>((min(rows_valid, ROWS) - 1) * row_stride + D) * 2u : 0u;
-    const auto r = make_rsrc(base, bytes);
-    const int rr = lane / CH;
-#pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-        const int blk = wave * IPW + i;
-        const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * RPB + rr);
-        // Whole offset in voffset: the range check that zero-fills rows past the
-        // end covers voffset only.
-        load_lds16(r, tile + blk * 512, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u, 0);
-    }
-}
-
-// Per-lane parts of the swizzled tile addresses. The swizzle of a row depends
-// only on row % (CH) bits that the compile-time parts of the reads (32-row
-// halves, 16-row groups) leave unchanged, so each read is the lane base plus a
-// constant row offset plus 8 * (constant chunk ^ lane chunk key): one XOR.
-template <int D>
-struct TileLane {
-    int rm_base;   // row-major read: row l32
-    int rm_key;    // chunk key: hh ^ swizzle(l32)
-    int tr_base;   // transposed read: row 4hh + li/4, 4-element half li & 1
-    int tr_key_lo; // chunk key of that row: (2 g16 + (li & 3) / 2) ^ swizzle(row)
-    int tr_key_hi; // same for the row 8 further down
-
-    __device__ __forceinline__ TileLane(int lane) {
-        constexpr int CH = D / 8;
-        const int l32 = lane & 31, hh = lane >> 5, g16 = (lane >> 4) & 1, li = lane & 15;
-        rm_base = l32 * D;
-        rm_key = hh ^ kv_swizzle<CH>(l32);
-        const int r0 = 4 * hh + (li >> 2);
-        const int y = 2 * g16 + ((li & 3) >> 1);
-        tr_base = r0 * D + 4 * (li & 1);
-        tr_key_lo = y ^ kv_swizzle<CH>(r0);
-        tr_key_hi = y ^ kv_swizzle<CH>(r0 + 8);
-    }
-    // Hides the keys from loop-invariant hoisting: each read then costs one XOR
-    // instead of a register holding its precomputed address.
-    __device__ __forceinline__ void refresh() {
-        asm volatile("" : "+v"(rm_key), "+v"(tr_key_lo), "+v"(tr_key_hi));
-    }
-    // Row-major 16-byte read of row 32 * half + l32, chunk 2 * ks + hh.
-    __device__ __forceinline__ u32x4 rm(const uint16_t* tile, int half, int ks) const {
-        return *reinterpret_cast<const u32x4*>(tile + rm_base + 32 * half * D + 8 * ((2 * ks) ^ rm_key));
-    }
-    // A operand of X^T = M^T P: element (d, r) = tile[16 tt + r][32 db + d], read
-    // transposed from rows 16tt + 4hh + li/4 and + 8.
-    __device__ __forceinline__ u32x4 tr(const uint16_t* tile, int db, int tt) const {
-        const uint16_t* p = tile + tr_base + 16 * tt * D;
-        const uint2 lo = ds_read_tr16(p + 8 * ((4 * db) ^ tr_key_lo));
-        const uint2 hi = ds_read_tr16(p + 8 * D + 8 * ((4 * db) ^ tr_key_hi));
-        return u32x4{lo.x, lo.y, hi.x, hi.y};
-    }
-};
-
 template <typename T, int D, int NW, bool VARLEN>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {
     constexpr int BN = 64;
@@ -1051,30 +981,15 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
     }
 }
 
-int bwd_override() {
-    const char* e = std::getenv("KCR_FA_BWD_V1");
-    return e ? std::atoi(e) : 0;
-}
-
 template <typename T, int D, bool VARLEN, bool GEN>
 void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
     if constexpr (!GEN && (D == 64 || D == 128)) {
         // The tiled kernels need the full bucket width and 32-bit tile offsets.
         constexpr int64_t kMaxStride = int64_t{1} << 23;
-        const bool fits = prm.head_dim == D && prm.q_s <= kMaxStride && prm.k_s <= kMaxStride &&
-                          prm.v_s <= kMaxStride && prm.do_s <= kMaxStride;
-        if (fits && !bwd_override()) {
-            const char* w = std::getenv("KCR_FA_BWD_WAVES");
-            const int waves = w ? std::atoi(w) : 4;
-            if (waves == 8) {
-                launch_bwd_v2<T, D, VARLEN, 8, 8>(prm, want_q, want_kv, s);
-            } else if (waves == 48) {
-                launch_bwd_v2<T, D, VARLEN, 4, 8>(prm, want_q, want_kv, s);
-            } else if (waves == 84) {
-                launch_bwd_v2<T, D, VARLEN, 8, 4>(prm, want_q, want_kv, s);
-            } else {
-                launch_bwd_v2<T, D, VARLEN, 4, 4>(prm, want_q, want_kv, s);
-            }
+        auto ok = [&](int64_t st) { return st >= 0 && st <= kMaxStride; };
+        const bool fits = prm.head_dim == D && ok(prm.q_s) && ok(prm.k_s) && ok(prm.v_s) && ok(prm.do_s);
+        if (fits) {
+            launch_bwd_v2<T, D, VARLEN, 4, 4>(prm, want_q, want_kv, s);
             return;
         }
     }

@@ -8,9 +8,7 @@
 // sequence bounds from cu_seqlens), host/forward/mod.rs:52-853 and
 // host/varlen/mod.rs:21-670 (validation, window normalisation, empty inputs).
 //
-// MI355X design
-//   * One block = NW waves; each wave owns 32*QT query rows, so a block covers
-//     BM = 32*QT*NW rows of one (batch, head). Keys stream in tiles of BN = 64.
+// MI355X design (shared by both kernels of this file)
 //   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16
 //     (bf16 or f16): the accumulator layout puts one query per lane (lane % 32)
 //     and 16 keys per lane-half in registers, so the online-softmax row max is a
@@ -19,17 +17,18 @@
 //   * The exponentiated scores are already laid out as the B operand of
 //     O^T = V^T P^T: the accumulator registers are packed to bf16/f16 pairs in
 //     place, no LDS round trip for P.
-//   * Q stays in VGPRs for the whole key loop. K is staged row-major in LDS (one
-//     ds_read_b128 per MFMA operand); V is staged transposed ([d][key], two
-//     ds_read_b64 per operand), the transpose done by the loading threads in
-//     registers (4 keys x 8 d per thread -> eight 8-byte LDS stores).
-//   * The next K/V tile is fetched from HBM into registers while the current tile
-//     is consumed (register double-buffering); masks are evaluated only on tiles
-//     that cross a causal / window / sequence edge.
+//   * Q stays in VGPRs for the whole key loop; keys stream in tiles of 64.
+//   * Masks are evaluated only on tiles that cross a causal / window / sequence
+//     edge; the online softmax rescales O lazily (only when a row max grows by
+//     more than kRescaleSlack in log2 units).
 //   * Causal grids run the longest query tiles first, and the query heads sharing
 //     one KV head are placed on one XCD (blocks are dealt round-robin over the 8
 //     XCDs) so their K/V tiles hit the same L2.
-#include <cstdlib>
+//
+// flash_fwd_tiled_kernel (plain scaled dot product, head size 64 or 128) copies
+// K/V tiles HBM -> LDS with direct buffer loads into swizzled row-major tiles;
+// flash_fwd_kernel (softcap, ALiBi, other head sizes, non-positive scales)
+// stages the tiles through registers and stores V transposed.
 
 #include "attention.h"
 
@@ -426,46 +425,25 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 }
 
 // ---------------------------------------------------------------------------
-// Forward v3 (plain scaled dot product, head size 64 or 128): K and V tiles are
-// copied HBM -> LDS by direct buffer loads (no staging registers, no VALU).
-// LDS layout "4-key blocks": each wave-wide 16-byte-per-lane copy moves four
-// whole rows (keys 4j..4j+3, coalesced in HBM) into one block, stored
-// chunk-major inside the block (chunk c of key 4j+i at c*64 + 16*i bytes);
-// blocks are padded by 64 bytes. Then
-//   * K, the A operand of S^T = K Q^T, is one ds_read_b128 per operand at
-//     lane_base + immediate,
-//   * V^T, the A operand of O^T = V^T P^T, is read with ds_read_b64_tr_b16,
-//     which transposes 4 rows x 16 columns of 16-bit values inside each group
-//     of 16 lanes (lane i receives column i of the 4 rows): a group's 4 keys are
-//     one block and its two chunks are 128 contiguous bytes,
-// so no read needs per-tile address arithmetic and none conflicts on banks
-// (the padding puts neighbouring blocks 16 banks apart).
-// Two LDS stages; the next tile's copy is in flight during the current tile.
+// Tiled forward (plain scaled dot product, head size 64 or 128). One block =
+// 4 waves = 128 query rows of one head; each wave owns 32 rows, their Q in
+// registers as the B operand of S^T = K Q^T (one query per lane: the row max and
+// sum are in-lane reductions plus one cross-half shuffle). K and V tiles of 64
+// keys are copied HBM -> LDS by direct buffer loads into row-major tiles with
+// XOR-swizzled 16-byte chunks (no staging registers, no VALU); K is read with
+// ds_read_b128 and V^T, the A operand of O^T = V^T P^T, with ds_read_b64_tr_b16
+// from the same row-major tile. P^T stays in registers: the fp32 scores are
+// packed in place into the B operand of the PV MFMA. Two LDS stages, the next
+// tile's copy in flight during the current tile, one barrier per tile.
 // ---------------------------------------------------------------------------
-// LAYOUT 1: 4-key blocks (above). LAYOUT 0: row-major rows with the chunks of
-// each row XOR-swizzled by kv_swizzle (one 1 KB copy = 4 rows; addresses of the
-// reads need per-lane XOR arithmetic).
-template <typename T, int D, int QT, int NW, bool VARLEN, int LAYOUT>
-__global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParams p) {
+template <typename T, int D, bool VARLEN>
+__global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams p) {
+    constexpr int NW = 4;
     constexpr int BN = kBN;
-    constexpr int BM = 32 * QT * NW;
+    constexpr int BM = 32 * NW;
     constexpr int KS = D / 16;
     constexpr int DB = D / 32;
-    constexpr int CH = D / 8;               // 16-byte chunks per row
-    constexpr int KPB = 64 / CH;            // keys per 1 KB block (4 for D = 128)
-    constexpr int BLK = LAYOUT == 0 ? 512 : 512 + 32;  // block stride (elements): 1 KB (+ 64 B)
-    constexpr int NBLK = BN / KPB;          // blocks per tile
-    constexpr int TILE = NBLK * BLK;        // elements per K or V tile
-    constexpr int IPW = NBLK / NW;          // blocks each wave copies per tile
-    static_assert(NBLK % NW == 0, "tile blocks must split evenly over the waves");
-    // Element offset of (key, chunk c) in a tile.
-    auto kv_at = [](int key, int c) {
-        if constexpr (LAYOUT == 0) {
-            return key * D + 8 * (c ^ kv_swizzle<CH>(key));
-        } else {
-            return (key / KPB) * BLK + c * (8 * KPB) + 8 * (key % KPB);
-        }
-    };
+    constexpr int TILE = BN * D;
 
     __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2 * TILE];
     __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2 * TILE];
@@ -475,7 +453,10 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
     const int wave = tid >> 6;
     const int l32 = lane & 31;
     const int hh = lane >> 5;
+    TileLane<D> tl(lane);
 
+    // Query-tile-major grid, longest causal tiles first; with xcd_groups the
+    // query heads of one KV head share blockIdx % 8, i.e. one XCD and its L2.
     const int per_tile = p.batch * p.heads;
     const int qo = blockIdx.x / per_tile;
     const int rem = blockIdx.x - qo * per_tile;
@@ -492,8 +473,8 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
     const int b = bh / p.heads;
     const int head = bh - b * p.heads;
     const int kvh = head / p.gqa;
-    // Longest causal tiles first: block qo takes the qo-th query tile counted
-    // from the end of its own sequence (varlen sequences end at different tiles).
+    // Block qo takes the qo-th query tile counted from the end of its sequence
+    // (varlen sequences end at different tiles).
     int qb = p.q_blocks - 1 - qo;
 
     int64_t q_off = 0, k_off = 0;
@@ -547,57 +528,25 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
     int kv_begin = 0;
     if (wl >= 0) kv_begin = (max(0, min(sk, row0 + off - wl)) / BN) * BN;
 
-    const int wrow0 = row0 + wave * 32 * QT;
-    u32x4 qf[QT][KS];
+    const int row = row0 + wave * 32 + l32;
+    u32x4 qf[KS];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const int row = wrow0 + qt * 32 + l32;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            qf[qt][ks] = row < sq ? *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + 16 * ks + 8 * hh)
-                                  : u32x4{0, 0, 0, 0};
-        }
+    for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = row < sq ? *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + 16 * ks + 8 * hh)
+                          : u32x4{0, 0, 0, 0};
     }
     const float c = p.scale_log2;
 
-    f32x16 o[QT][DB];
-    float m[QT], l[QT];
+    f32x16 o[DB];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        m[qt] = -INFINITY;
-        l[qt] = 0.0f;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[qt][db] = f32x16{};
-    }
+    for (int db = 0; db < DB; ++db) o[db] = f32x16{};
+    float m = -INFINITY, l = 0.0f;
 
-    // Lane i of a block copy moves chunk i / KPB of key i % KPB; the block's
-    // first row goes in the scalar offset.
-    const uint32_t krow_bytes = static_cast<uint32_t>(p.k_s) * 2u;
-    const uint32_t vrow_bytes = static_cast<uint32_t>(p.v_s) * 2u;
-    // (LAYOUT 0 recomputes the swizzled source chunk per block in copy_tile.)
-    const uint32_t k_src = static_cast<uint32_t>(lane % KPB) * krow_bytes + (lane / KPB) * 16u;
-    const uint32_t v_src = static_cast<uint32_t>(lane % KPB) * vrow_bytes + (lane / KPB) * 16u;
     auto copy_tile = [&](int kb, int stage) {
-        const int rows = min(sk - kb, BN);
-        const uint32_t kbytes = static_cast<uint32_t>((rows - 1) * p.k_s + D) * 2u;
-        const uint32_t vbytes = static_cast<uint32_t>((rows - 1) * p.v_s + D) * 2u;
-        const auto kr = make_rsrc(kbase + static_cast<int64_t>(kb) * p.k_s, kbytes);
-        const auto vr = make_rsrc(vbase + static_cast<int64_t>(kb) * p.v_s, vbytes);
-#pragma unroll
-        for (int i = 0; i < IPW; ++i) {
-            const int blk = wave * IPW + i;
-            uint32_t ks_off = k_src, vs_off = v_src;
-            if constexpr (LAYOUT == 0) {
-                const int r = lane / CH;
-                const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * KPB + r);
-                ks_off = static_cast<uint32_t>(r) * krow_bytes + gc * 16u;
-                vs_off = static_cast<uint32_t>(r) * vrow_bytes + gc * 16u;
-            }
-            // The whole offset goes in voffset: the hardware range check that
-            // zero-fills rows past the sequence end covers voffset only.
-            load_lds16(kr, k_lds + stage * TILE + blk * BLK, ks_off + blk * KPB * krow_bytes, 0);
-            load_lds16(vr, v_lds + stage * TILE + blk * BLK, vs_off + blk * KPB * vrow_bytes, 0);
-        }
+        copy_rows<D, NW, BN>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE,
+                             wave, lane);
+        copy_rows<D, NW, BN>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE,
+                             wave, lane);
     };
 
     const int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
@@ -607,125 +556,85 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
         __syncthreads();
     }
 
-    // Lane-constant parts of the LDS read addresses.
-    const int g16 = (lane >> 4) & 1;  // which 16 of the 32 d in an O^T block
-    const int li = lane & 15;
-
     for (int t = 0; t < ntiles; ++t) {
         const int kb = kv_begin + t * BN;
         const uint16_t* kl = k_lds + (t & 1) * TILE;
         const uint16_t* vl = v_lds + (t & 1) * TILE;
         if (t + 1 < ntiles) copy_tile(kb + BN, (t + 1) & 1);
 
-        f32x16 s[QT][2];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            s[qt][0] = f32x16{};
-            s[qt][1] = f32x16{};
-        }
+        // S^T = K Q^T for the 64 keys of the tile (two 32-key halves).
+        f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const u32x4 ka0 = *reinterpret_cast<const u32x4*>(kl + kv_at(l32, 2 * ks + hh));
-            const u32x4 ka1 = *reinterpret_cast<const u32x4*>(kl + kv_at(32 + l32, 2 * ks + hh));
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                s[qt][0] = mfma32<T>(ka0, qf[qt][ks], s[qt][0]);
-                s[qt][1] = mfma32<T>(ka1, qf[qt][ks], s[qt][1]);
-            }
+            s[0] = mfma32<T>(tl.rm(kl, 0, ks), qf[ks], s[0]);
+            s[1] = mfma32<T>(tl.rm(kl, 1, ks), qf[ks], s[1]);
         }
 
         const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
                                (wl >= 0 && kb < last_row + off - wl);
-        u32x4 pk[QT][4];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const int row = wrow0 + qt * 32 + l32;
-            if (need_mask) {
-#pragma unroll
-                for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
-                        const bool masked = (col >= sk) | (wr >= 0 & col > row + off + wr) |
-                                            (wl >= 0 & col < row + off - wl);
-                        s[qt][sub][r] = masked ? -INFINITY : s[qt][sub][r];
-                    }
-                }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[qt][sub][r], s[qt][sub][r + 1]));
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m2 = mx * c;
-            if (__any(m2 > m[qt] + kRescaleSlack)) {
-                const float m_new = fmaxf(m[qt], m2);
-                const float alpha = (m_new == -INFINITY) ? 1.0f : fast_exp2(m[qt] - m_new);
-                m[qt] = m_new;
-                l[qt] *= alpha;
-#pragma unroll
-                for (int db = 0; db < DB; ++db) o[qt][db] *= alpha;
-            }
-            const float neg_m = (m[qt] == -INFINITY) ? 0.0f : -m[qt];
-            float rowsum = 0.0f;
+        if (need_mask) {
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float pv = fast_exp2(__builtin_fmaf(s[qt][sub][r], c, neg_m));
-                    s[qt][sub][r] = pv;
-                    rowsum += pv;
-                }
-            }
-            l[qt] += rowsum;
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const int sub = tt >> 1;
-                const int base = 8 * (tt & 1);
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    pk[qt][tt][w] = pack2<T>(s[qt][sub][base + 2 * w], s[qt][sub][base + 2 * w + 1]);
+                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    const bool masked = (col >= sk) | (wr >= 0 & col > row + off + wr) |
+                                        (wl >= 0 & col < row + off - wl);
+                    s[sub][r] = masked ? -INFINITY : s[sub][r];
                 }
             }
         }
-
-        // ---- O^T += V^T P^T, V^T read transposed from the key-major planes ----
-        // Lane part of the transposing reads: key 4*hh + li/4 of each 16-key group,
-        // chunk 2*g16 + (li & 3)/2 of each 32-wide d block, 8-byte half li & 1.
-        const uint16_t* vlane = vl + kv_at(4 * hh + (li >> 2), 2 * g16 + ((li & 3) >> 1)) + 4 * (li & 1);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[sub][r], s[sub][r + 1]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m2 = mx * c;
+        // Lazy rescale: the running max moves only when some row's max grows by
+        // more than the slack (wave-uniform decision).
+        if (__any(m2 > m + kRescaleSlack)) {
+            const float m_new = fmaxf(m, m2);
+            const float alpha = (m_new == -INFINITY) ? 1.0f : fast_exp2(m - m_new);
+            m = m_new;
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[db] *= alpha;
+        }
+        const float neg_m = (m == -INFINITY) ? 0.0f : -m;
+        float rowsum = 0.0f;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pv = fast_exp2(__builtin_fmaf(s[sub][r], c, neg_m));
+                s[sub][r] = pv;
+                rowsum += pv;
+            }
+        }
+        l += rowsum;
+        // P^T packed in place: k-slot j of group tt is key 16tt + 8(j/4) + 4hh + j%4.
+        u32x4 pk[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                pk[tt][w] = pack2<T>(s[tt >> 1][8 * (tt & 1) + 2 * w], s[tt >> 1][8 * (tt & 1) + 2 * w + 1]);
+            }
+        }
+        // O^T += V^T P^T
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const uint16_t* va_p;
-                const uint16_t* vb_p;
-                if constexpr (LAYOUT == 0) {
-                    const int key = 16 * tt + 4 * hh + (li >> 2);
-                    const int gc = 4 * db + 2 * g16 + ((li & 3) >> 1);
-                    va_p = vl + kv_at(key, gc) + 4 * (li & 1);
-                    vb_p = vl + kv_at(key + 8, gc) + 4 * (li & 1);
-                } else {
-                    va_p = vlane + kv_at(16 * tt, 4 * db);
-                    vb_p = va_p + kv_at(8, 0);
-                }
-                const uint2 lo = ds_read_tr16(va_p);
-                const uint2 hi = ds_read_tr16(vb_p);
-                const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) o[qt][db] = mfma32<T>(va, pk[qt][tt], o[qt][db]);
-            }
+            for (int tt = 0; tt < 4; ++tt) o[db] = mfma32<T>(tl.tr(vl, db, tt), pk[tt], o[db]);
         }
         wait_vmem();
         __syncthreads();
     }
 
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const int row = wrow0 + qt * 32 + l32;
-        const float lt = l[qt] + __shfl_xor(l[qt], 32, 64);
-        if (row >= sq) continue;
+    const float lt = l + __shfl_xor(l, 32, 64);
+    if (row < sq) {
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         uint16_t* orow = obase + row * p.o_s;
 #pragma unroll
@@ -734,12 +643,12 @@ __global__ void __launch_bounds__(NW * 64, 2) flash_fwd_v3_kernel(const FwdParam
             for (int g = 0; g < 4; ++g) {
                 const int d = 32 * db + 8 * g + 4 * hh;
                 uint2 w;
-                w.x = pack2<T>(o[qt][db][4 * g] * inv, o[qt][db][4 * g + 1] * inv);
-                w.y = pack2<T>(o[qt][db][4 * g + 2] * inv, o[qt][db][4 * g + 3] * inv);
+                w.x = pack2<T>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+                w.y = pack2<T>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
                 *reinterpret_cast<uint2*>(orow + d) = w;
             }
         }
-        if (hh == 0) lse_base[row] = lt > 0.0f ? (m[qt] + fast_log2(lt)) * kLn2 : INFINITY;
+        if (hh == 0) lse_base[row] = lt > 0.0f ? (m + fast_log2(lt)) * kLn2 : INFINITY;
     }
 }
 
@@ -810,20 +719,15 @@ void launch_cfg(FwdParams& prm, bool general, hipStream_t s) {
     check_launch("launch flash_fwd");
 }
 
-int tile_override() {
-    const char* e = std::getenv("KCR_FA_FWD_TILE");
-    return e ? std::atoi(e) : 0;
-}
-
-template <typename T, int D, int QT, int NW, bool VARLEN, int LAYOUT>
-void launch_v3(FwdParams& prm, hipStream_t s) {
-    constexpr int BM = 32 * QT * NW;
+template <typename T, int D, bool VARLEN>
+void launch_tiled(FwdParams& prm, hipStream_t s) {
+    constexpr int BM = 128;
     prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
     const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads;
     if (blocks == 0) return;
     if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
     prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
-    flash_fwd_v3_kernel<T, D, QT, NW, VARLEN, LAYOUT><<<static_cast<unsigned>(blocks), NW * 64, 0, s>>>(prm);
+    flash_fwd_tiled_kernel<T, D, VARLEN><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
     check_launch("launch flash_fwd");
 }
 
@@ -831,11 +735,7 @@ template <typename T, int D, bool VARLEN>
 void launch_d(FwdParams& prm, bool general, hipStream_t s) {
     if constexpr (D == 64 || D == 128) {
         if (!general) {
-            switch (tile_override()) {
-                case 1: break;  // the v2 kernel
-                case 4: return launch_v3<T, D, 1, 4, VARLEN, 1>(prm, s);
-                default: return launch_v3<T, D, 1, 4, VARLEN, 0>(prm, s);
-            }
+            return launch_tiled<T, D, VARLEN>(prm, s);
         }
     }
     launch_cfg<T, D, 1, 4, VARLEN>(prm, general, s);
