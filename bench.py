@@ -6,9 +6,11 @@ A "step" is one call of an op over its BASELINE.json configuration with inputs
 already resident in HBM. The headline op (default: FA2 forward, causal, B=4
 Hq=32 Hkv=8 S=4096 D=128 bf16) gives `value`; every op
 measured is listed under "ops" with its own throughput and roofline fraction.
-Timing: HIP events recorded on the stream the kernels are launched on (torch's
-current stream, which the ops pass to the C ABI), around exactly K steps
-bracketed by torch.cuda.synchronize().
+Timing: W untimed warmup steps, then untimed steps for at least --warm-ms of
+wall time (the GPU's clocks settle under sustained load), then HIP events
+recorded on the stream the kernels are launched on (torch's current stream,
+which the ops pass to the C ABI) around exactly K steps, bracketed by
+torch.cuda.synchronize().
 
 Prints ONE JSON line.
 """
@@ -274,12 +276,19 @@ def cpu_attention(q, k, v, causal):
 # --------------------------------------------------------------------------
 
 
-def measure(name, steps, warmup):
+def measure(name, steps, warmup, warm_ms):
     wl = WORKLOADS[name]()
     run = wl["run"]
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
+    # Then untimed steps for at least warm_ms of wall time, so the timed steps
+    # see the GPU's sustained clocks rather than the ramp after input set-up.
+    t_end = time.perf_counter() + warm_ms * 1e-3
+    while time.perf_counter() < t_end:
+        for _ in range(max(1, steps // 4)):
+            run()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -300,8 +309,10 @@ def measure(name, steps, warmup):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warm-ms", type=float, default=300.0,
+                    help="after the warmup steps, keep stepping untimed for this long (ms)")
     ap.add_argument("--headline", default="fa_fwd_causal")
     ap.add_argument("--only", default=None, help="comma-separated workloads (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -322,7 +333,7 @@ def main():
     for name in names:
         log(f"[bench] {name} ...")
         try:
-            wl, ms, achieved, peak, unit = measure(name, args.steps, args.warmup)
+            wl, ms, achieved, peak, unit = measure(name, args.steps, args.warmup, args.warm_ms)
         except Exception as e:  # an op that is not built yet is reported, not fatal
             log(f"[bench] {name} failed: {type(e).__name__}: {e}")
             results[name] = {"error": f"{type(e).__name__}: {e}"}
