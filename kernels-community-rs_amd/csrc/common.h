@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <type_traits>
@@ -55,6 +56,22 @@ inline void check_hip(hipError_t status, const char* what) {
 
 // Checks the launch that was just enqueued.
 inline void check_launch(const char* what) { check_hip(hipGetLastError(), what); }
+
+// Compute units of the current device, queried once per device.
+inline int compute_units() {
+    static std::atomic<int> cached[64] = {};
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64) dev = 0;
+    int cu = cached[dev].load(std::memory_order_relaxed);
+    if (cu == 0) {
+        check_hip(hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev),
+                  "hipDeviceGetAttribute");
+        if (cu <= 0) cu = 1;
+        cached[dev].store(cu, std::memory_order_relaxed);
+    }
+    return cu;
+}
 
 // ---------------------------------------------------------------------------
 // Tensor metadata.

@@ -122,14 +122,22 @@ __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
         }
     }
 
-    for (uint32_t row = wave; row < rows; row += waves) {
-        const u32x4* xr = x + static_cast<uint64_t>(row) * nvec;
-        u32x4 xv[CHUNKS];
+    // Rows are dealt to waves round-robin; the next row's loads are issued
+    // before the current row is reduced and written, so every wave keeps a
+    // whole row of reads in flight.
+    auto load_row = [&](uint32_t r, u32x4 (&dst)[CHUNKS]) {
+        const u32x4* xr = x + static_cast<uint64_t>(r) * nvec;
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
             const uint32_t v = lane + 64u * c;
-            if (v < nvec) xv[c] = __builtin_nontemporal_load(xr + v);
+            if (v < nvec) dst[c] = __builtin_nontemporal_load(xr + v);
         }
+    };
+    u32x4 xv[CHUNKS];
+    if (wave < rows) load_row(wave, xv);
+    for (uint32_t row = wave; row < rows; row += waves) {
+        u32x4 xn[CHUNKS];
+        if (row + waves < rows) load_row(row + waves, xn);
         float sum = 0.0f;
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
@@ -165,6 +173,8 @@ __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
                 __builtin_nontemporal_store(narrow16<X>(o), yr + v);
             }
         }
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) xv[c] = xn[c];
     }
 }
 
@@ -350,8 +360,10 @@ template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
 void launch_wave(const Fwd& f, uint32_t nvec) {
     const uint64_t waves_needed = static_cast<uint64_t>(f.rows);
     uint64_t blocks = (waves_needed + kWaves - 1) / kWaves;
-    // One wave per row (the kernel loops if the grid is capped).
-    const uint64_t cap = 2147483647ull;
+    // Six blocks (24 waves) per CU, each wave looping over rows with one row
+    // prefetched: measured on MI355X at 16384 x 4096 bf16, 50 us for one
+    // wave per row vs 45.5 us for this shape.
+    const uint64_t cap = 6ull * compute_units();
     if (blocks > cap) blocks = cap;
     rms_fwd_wave<X, W, M, AFFINE, CHUNKS><<<static_cast<unsigned>(blocks), 64 * kWaves, 0, f.stream>>>(
         static_cast<u32x4*>(f.y->data), static_cast<float*>(f.rstd->data),
