@@ -88,6 +88,7 @@ struct FwdParams {
     int32_t window_left, window_right;
     int32_t q_blocks;            // query tiles per (batch, head)
     int32_t xcd_groups;          // 1: group the query heads of one KV head on one XCD
+    int32_t seq_major;           // 1: sequence-major block order (tiled kernel)
     int32_t alibi_b;             // alibi batch stride (0 for [H])
     int32_t alibi_causal;
     float scale_log2;            // softmax scale * log2(e), no softcap

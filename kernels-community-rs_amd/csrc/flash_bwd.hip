@@ -52,6 +52,7 @@ struct BwdParams {
     int32_t head_dim;
     int32_t window_left, window_right;
     int32_t blocks_per_seq;  // key blocks (dkv) or query blocks (dq) per (batch, head)
+    int32_t seq_major;       // varlen v2 kernels: sequence-major block order
     int32_t alibi_b, alibi_causal;
     float scale_log2;
     float tanh_scale;
@@ -597,14 +598,27 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     // query heads of one KV head share blockIdx % (B * Hk), hence one XCD when
     // B * Hk is a multiple of 8 (K/V tiles stay in that XCD's L2).
     const int per = p.blocks_per_seq;
-    const int nbh = p.batch * p.heads;
-    const int nbkv = p.batch * p.kv_heads;
-    const int qo = blockIdx.x / nbh;
-    const int idx = blockIdx.x - qo * nbh;
-    const int g = idx % nbkv;
-    const int b = g / p.kv_heads;
-    const int kvh = g - b * p.kv_heads;
-    const int head = kvh * p.gqa + idx / nbkv;
+    int b, kvh, head, qo;
+    if (p.seq_major) {
+        // Sequence-major: the blocks of one sequence run together and share its
+        // K/V tiles in L2; the query heads of one KV head keep one XCD.
+        const int nh = p.heads;
+        b = blockIdx.x / (per * nh);
+        const int rem = blockIdx.x - b * per * nh;
+        qo = rem / nh;
+        const int idx = rem - qo * nh;
+        kvh = idx % p.kv_heads;
+        head = kvh * p.gqa + idx / p.kv_heads;
+    } else {
+        const int nbh = p.batch * p.heads;
+        const int nbkv = p.batch * p.kv_heads;
+        qo = blockIdx.x / nbh;
+        const int idx = blockIdx.x - qo * nbh;
+        const int g = idx % nbkv;
+        b = g / p.kv_heads;
+        kvh = g - b * p.kv_heads;
+        head = kvh * p.gqa + idx / nbkv;
+    }
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
@@ -757,11 +771,21 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
 
     // Tile-major order: the key tiles that see the most causal queries start
     // first across the whole grid; one (batch, KV head) keeps one XCD.
-    const int nbkv = p.batch * p.kv_heads;
-    const int kbi = blockIdx.x / nbkv;
-    const int bkv = blockIdx.x - kbi * nbkv;
-    const int b = bkv / p.kv_heads;
-    const int kvh = bkv - b * p.kv_heads;
+    int b, kvh, kbi;
+    if (p.seq_major) {
+        // Sequence-major (see the dQ kernel): key tiles of one sequence together.
+        const int per = p.blocks_per_seq;
+        b = blockIdx.x / (per * p.kv_heads);
+        const int rem = blockIdx.x - b * per * p.kv_heads;
+        kbi = rem / p.kv_heads;
+        kvh = rem - kbi * p.kv_heads;
+    } else {
+        const int nbkv = p.batch * p.kv_heads;
+        kbi = blockIdx.x / nbkv;
+        const int bkv = blockIdx.x - kbi * nbkv;
+        b = bkv / p.kv_heads;
+        kvh = bkv - b * p.kv_heads;
+    }
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
@@ -989,6 +1013,11 @@ void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
         auto ok = [&](int64_t st) { return st >= 0 && st <= kMaxStride; };
         const bool fits = prm.head_dim == D && ok(prm.q_s) && ok(prm.k_s) && ok(prm.v_s) && ok(prm.do_s);
         if (fits) {
+            // Sequence-major block order when every block of a sequence does the
+            // same work (no causal / window mask) or the sequences are packed:
+            // concurrent blocks then share one sequence's tiles in L2. Masked
+            // dense grids keep the tile-major, longest-first order.
+            prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
             launch_bwd_v2<T, D, VARLEN, 4, 4>(prm, want_q, want_kv, s);
             return;
         }

@@ -457,21 +457,34 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
 
     // Query-tile-major grid, longest causal tiles first; with xcd_groups the
     // query heads of one KV head share blockIdx % 8, i.e. one XCD and its L2.
-    const int per_tile = p.batch * p.heads;
-    const int qo = blockIdx.x / per_tile;
-    const int rem = blockIdx.x - qo * per_tile;
-    int bh;
-    if (p.xcd_groups) {
-        const int xcd = rem & 7;
-        const int rr = rem >> 3;
-        const int j = rr % p.gqa;
-        const int g = (rr / p.gqa) * 8 + xcd;
-        bh = g * p.gqa + j;
+    int b, head, qo;
+    if (p.seq_major) {
+        // Sequence-major (unmasked or packed grids): the blocks of one sequence
+        // run together and share its K/V tiles in L2; the query heads of one KV
+        // head keep one XCD when Hk is a multiple of 8.
+        const int per_seq = p.q_blocks * p.heads;
+        b = blockIdx.x / per_seq;
+        const int rem = blockIdx.x - b * per_seq;
+        qo = rem / p.heads;
+        const int idx = rem - qo * p.heads;
+        head = (idx % p.kv_heads) * p.gqa + idx / p.kv_heads;
     } else {
-        bh = rem;
+        const int per_tile = p.batch * p.heads;
+        qo = blockIdx.x / per_tile;
+        const int rem = blockIdx.x - qo * per_tile;
+        int bh;
+        if (p.xcd_groups) {
+            const int xcd = rem & 7;
+            const int rr = rem >> 3;
+            const int j = rr % p.gqa;
+            const int g = (rr / p.gqa) * 8 + xcd;
+            bh = g * p.gqa + j;
+        } else {
+            bh = rem;
+        }
+        b = bh / p.heads;
+        head = bh - b * p.heads;
     }
-    const int b = bh / p.heads;
-    const int head = bh - b * p.heads;
     const int kvh = head / p.gqa;
     // Block qo takes the qo-th query tile counted from the end of its sequence
     // (varlen sequences end at different tiles).
@@ -727,6 +740,9 @@ void launch_tiled(FwdParams& prm, hipStream_t s) {
     if (blocks == 0) return;
     if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
     prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
+    // Sequence-major order for packed sequences and unmasked grids (blocks of
+    // equal work); masked dense grids keep the longest-first tile-major order.
+    prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
     flash_fwd_tiled_kernel<T, D, VARLEN><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
     check_launch("launch flash_fwd");
 }
