@@ -64,8 +64,11 @@ def _scores(q, k, scale, softcap, alibi_slopes, causal, wl, wr):
 
 
 def forward(q, k, v, *, softmax_scale=None, causal=False, window_left=-1, window_right=-1,
-            softcap=0.0, alibi_slopes=None, dtype=np.float32):
-    """Dense attention. q [B,Sq,H,D], k/v [B,Sk,Hk,D] -> out [B,Sq,H,D], lse [B,H,Sq]."""
+            softcap=0.0, alibi_slopes=None, dtype=np.float32, dropout_mask=None, p_dropout=0.0):
+    """Dense attention. q [B,Sq,H,D], k/v [B,Sk,Hk,D] -> out [B,Sq,H,D], lse [B,H,Sq].
+    With dropout (mask [B,H,Sq,Sk] of kept elements, oracle.dropout): out =
+    ((P * mask) / keep) V, keep = 1 - p (device/forward/mod.rs:1353, 1404); the LSE
+    is that of the undropped scores."""
     q = np.asarray(q, dtype=dtype)
     k = np.asarray(k, dtype=dtype)
     v = np.asarray(v, dtype=dtype)
@@ -81,6 +84,8 @@ def forward(q, k, v, *, softmax_scale=None, causal=False, window_left=-1, window
     e = np.exp(s - m)
     l = np.sum(e, axis=-1, keepdims=True)
     p = np.where(l > 0, e / np.where(l > 0, l, 1), 0)
+    if dropout_mask is not None:
+        p = p * dropout_mask / (np.float32(1.0) - np.float32(p_dropout))
     vh = np.repeat(np.transpose(v, (0, 2, 1, 3)), H // Hk, axis=1)
     out = np.transpose(p @ vh, (0, 2, 1, 3))
     lse = np.where(l[..., 0] > 0, m[..., 0] + np.log(np.where(l[..., 0] > 0, l[..., 0], 1)), np.inf)
@@ -88,18 +93,23 @@ def forward(q, k, v, *, softmax_scale=None, causal=False, window_left=-1, window
 
 
 def backward(q, k, v, out, dout, lse, *, softmax_scale=None, causal=False, window_left=-1,
-             window_right=-1, softcap=0.0, alibi_slopes=None, dtype=np.float32):
+             window_right=-1, softcap=0.0, alibi_slopes=None, dtype=np.float32, dropout_mask=None,
+             p_dropout=0.0):
     """Gradients of `forward`: returns dq [B,Sq,H,D], dk/dv [B,Sk,Hk,D] (GQA-summed)
-    and delta [B,H,Sq]."""
+    and delta [B,H,Sq]. With dropout, delta is keep * rowsum(dO * O) as the
+    reference's preprocess writes it (device/backward/reduce.rs:40-108), and the
+    gradients are those of the dropped forward: dV = (P*M/keep)^T dO,
+    dS = P * (dP*M/keep - rowsum(dO * O))."""
     q, k, v, out, dout = (np.asarray(x, dtype=dtype) for x in (q, k, v, out, dout))
     lse = np.asarray(lse, dtype=dtype)
     B, Sq, H, D = q.shape
     Sk, Hk = k.shape[1], k.shape[2]
     g = H // Hk
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else softmax_scale
+    keep = np.float32(1.0) - np.float32(p_dropout) if dropout_mask is not None else np.float32(1.0)
     delta = np.sum(dout * out, axis=-1).transpose(0, 2, 1)  # B H Sq
     if Sk == 0 or Sq == 0:
-        return np.zeros_like(q), np.zeros_like(k), np.zeros_like(v), delta
+        return np.zeros_like(q), np.zeros_like(k), np.zeros_like(v), keep * delta
     s, t, mask = _scores(q, k, scale, softcap, alibi_slopes, causal, window_left, window_right)
     finite = np.isfinite(lse)[..., None]
     p = np.where(finite & ~mask, np.exp(s - np.where(finite, lse[..., None], 0)), 0)
@@ -108,16 +118,20 @@ def backward(q, k, v, out, dout, lse, *, softmax_scale=None, causal=False, windo
     kh = np.repeat(np.transpose(k, (0, 2, 1, 3)), g, axis=1)
     vh = np.repeat(np.transpose(v, (0, 2, 1, 3)), g, axis=1)
     dp = doh @ np.swapaxes(vh, -1, -2)
+    pv = p
+    if dropout_mask is not None:
+        dp = dp * dropout_mask / keep
+        pv = p * dropout_mask / keep
     ds = p * (dp - delta[..., None])
     if t is not None:
         ds = ds * (1 - t * t)
     dqh = scale * (ds @ kh)
     dkh = scale * (np.swapaxes(ds, -1, -2) @ qh)
-    dvh = np.swapaxes(p, -1, -2) @ doh
+    dvh = np.swapaxes(pv, -1, -2) @ doh
     dk = dkh.reshape(B, Hk, g, Sk, D).sum(axis=2)
     dv = dvh.reshape(B, Hk, g, Sk, D).sum(axis=2)
     return (np.transpose(dqh, (0, 2, 1, 3)).astype(dtype), np.transpose(dk, (0, 2, 1, 3)).astype(dtype),
-            np.transpose(dv, (0, 2, 1, 3)).astype(dtype), delta.astype(dtype))
+            np.transpose(dv, (0, 2, 1, 3)).astype(dtype), (keep * delta).astype(dtype))
 
 
 def _slices(cu):
@@ -125,8 +139,23 @@ def _slices(cu):
     return [(cu[i], cu[i + 1]) for i in range(len(cu) - 1)]
 
 
+def _varlen_dropout(kw, b, H, sq, sk):
+    """Per-sequence keep mask for `dropout=(seed, offset, p)`: head bh = b*H + h,
+    rows and columns counted from the sequence start."""
+    from oracle import dropout as DR
+
+    drop = kw.get("dropout")
+    if drop is None:
+        return {}
+    seed, offset, p = drop
+    mask = np.stack([DR.keep_mask(seed, offset, b * H + h, sq, sk, p) for h in range(H)])[None]
+    return {"dropout_mask": mask, "p_dropout": p}
+
+
 def varlen_forward(q, k, v, cu_q, cu_k, **kw):
-    """Packed attention: q [Tq,H,D], k/v [Tk,Hk,D] -> out [Tq,H,D], lse [H,Tq]."""
+    """Packed attention: q [Tq,H,D], k/v [Tk,Hk,D] -> out [Tq,H,D], lse [H,Tq].
+    `dropout=(seed, offset, p)` applies the reference's mask stream per sequence."""
+    kw = dict(kw)
     dtype = kw.get("dtype", np.float32)
     q = np.asarray(q, dtype=dtype)
     Tq, H, D = q.shape
@@ -137,8 +166,10 @@ def varlen_forward(q, k, v, cu_q, cu_k, **kw):
         if qe == qs:
             continue
         slopes = None if alibi is None else (np.asarray(alibi)[b] if np.ndim(alibi) == 2 else alibi)
+        extra = _varlen_dropout(kw, b, H, qe - qs, ke - ks)
+        rest = {key: val for key, val in kw.items() if key != "dropout"}
         o, l = forward(q[None, qs:qe], np.asarray(k)[None, ks:ke], np.asarray(v)[None, ks:ke],
-                       alibi_slopes=slopes, **kw)
+                       alibi_slopes=slopes, **rest, **extra)
         out[qs:qe] = o[0]
         lse[:, qs:qe] = l[0]
     return out, lse
@@ -157,8 +188,10 @@ def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, **kw):
     for b, ((qs, qe), (ks, ke)) in enumerate(zip(_slices(cu_q), _slices(cu_k))):
         if qe == qs:
             continue
+        extra = _varlen_dropout(kw, b, H, qe - qs, ke - ks)
+        rest = {key: val for key, val in kw.items() if key != "dropout"}
         a, b_, c, d = backward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke], out[None, qs:qe],
-                               dout[None, qs:qe], np.asarray(lse)[None, :, qs:qe], **kw)
+                               dout[None, qs:qe], np.asarray(lse)[None, :, qs:qe], **rest, **extra)
         dq[qs:qe] = a[0]
         dk[ks:ke] += b_[0]
         dv[ks:ke] += c[0]
