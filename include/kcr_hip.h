@@ -121,14 +121,30 @@ int kcr_rms_norm_reduce_weight_grad(const kcr_tensor* dw, const kcr_tensor* dw_p
  *   alibi           : float32 [H] or [B, H] slopes, nullable
  */
 
+/* Dropout arguments of the attention entry points (NULL = no dropout). p in
+ * [0, 1) as float32; p == 0 disables it. The mask is FlashAttention-2's
+ * Philox4x32-7 stream (flash-attn2-rs/src/device/dropout.rs:31-121) keyed by
+ * (seed, offset): element (query q, key k) of head b * H + h is kept when byte
+ * ((q % 16) / 8 * 2 + k % 2) of word (k % 32) / 8 of
+ * philox(seed, offset + 32 (b H + h) + 4 (q % 8) + (k % 8) / 2, q / 16, k / 32) is at
+ * most floor((1 - p) * 255). With rng_state (a device int64 [2] tensor holding
+ * [seed, offset], read by the kernels on the launch stream) the seed and offset
+ * fields must be 0 and are ignored (host/forward/mod.rs:91-131). */
+typedef struct kcr_dropout {
+    double p;
+    uint64_t seed;
+    uint64_t offset;
+    const kcr_tensor* rng_state;  /* nullable */
+} kcr_dropout;
+
 /* Dense forward. replaces `fwd_lse(q,k,v,alibi,scale,causal,wl,wr,softcap,out)`
- * (flash-attn2-rs/src/host/forward/mod.rs:835-853; arities mod.rs:53-61) and the
- * p_dropout == 0 form of `fwd` (mod.rs:815-833).
+ * (flash-attn2-rs/src/host/forward/mod.rs:835-853; arities mod.rs:53-61) and `fwd`
+ * (mod.rs:815-833); dropout as in mod.rs:73-199 (return_softmax excluded).
  *   q [B,Sq,H,D], k/v [B,Sk,Hk,D] fp16/bf16, last stride 1;
  *   out like q (written), lse float32 contiguous [B,H,Sq] (written). */
 int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                   const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                  int64_t window_left, int64_t window_right, double softcap,
+                  int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                   const kcr_tensor* out, const kcr_tensor* lse, void* stream);
 
 /* Varlen forward. replaces the plain (non-paged, non-cached, p == 0) form of
@@ -141,7 +157,7 @@ int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_ten
                          const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
                          const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
                          const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                         int64_t window_left, int64_t window_right, double softcap,
+                         int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                          int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
                          const kcr_tensor* out, const kcr_tensor* lse, void* stream);
 
@@ -161,7 +177,7 @@ int64_t kcr_flash_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seql
 int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                   const kcr_tensor* dout, const kcr_tensor* lse, const kcr_tensor* delta,
                   const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                  int64_t window_left, int64_t window_right, double softcap,
+                  int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                   const kcr_tensor* dq, const kcr_tensor* dk, const kcr_tensor* dv,
                   void* workspace, int64_t workspace_bytes, void* stream);
 
@@ -174,7 +190,7 @@ int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_ten
                          const kcr_tensor* dout, const kcr_tensor* out, const kcr_tensor* lse,
                          const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
                          const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                         int64_t window_left, int64_t window_right, double softcap,
+                         int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                          int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
                          const kcr_tensor* dq, const kcr_tensor* dk, const kcr_tensor* dv,
                          const kcr_tensor* delta, void* workspace, int64_t workspace_bytes,

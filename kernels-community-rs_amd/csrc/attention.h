@@ -91,6 +91,10 @@ struct FwdParams {
     int32_t seq_major;           // 1: sequence-major block order (tiled kernel)
     int32_t alibi_b;             // alibi batch stride (0 for [H])
     int32_t alibi_causal;
+    const int64_t* rng_state;    // dropout: device [seed, offset], or null (use the fields below)
+    uint64_t drop_seed, drop_offset;
+    uint32_t drop_threshold;     // keep when byte <= threshold; 255 = no dropout
+    float inv_keep;              // 1 / (1 - p)
     float scale_log2;            // softmax scale * log2(e), no softcap
     float tanh_scale;            // softcap: tanh(raw * tanh_scale) * scale_eff
     float scale_eff_log2;        // softcap: softcap * sign(scale) * log2(e)
@@ -133,6 +137,52 @@ inline Options normalize_options(int has_scale, double scale, int causal, int64_
     o.window_left = static_cast<int32_t>(wl);
     o.window_right = static_cast<int32_t>(wr);
     return o;
+}
+
+// Dropout arguments (flash-attn2-rs/src/host/forward/mod.rs:73-131, 199): keep =
+// 1 - p in f32, threshold = floor(keep * 255) in f32, 255 = no dropout.
+struct DropoutArgs {
+    uint32_t threshold = 255;
+    float keep = 1.0f;
+    float inv_keep = 1.0f;
+    uint64_t seed = 0, offset = 0;
+    const int64_t* state = nullptr;
+};
+
+inline DropoutArgs parse_dropout(const kcr_dropout* d, double softcap, const kcr_tensor* q) {
+    DropoutArgs a;
+    if (!d) return a;
+    const double p = d->p;
+    if (!std::isfinite(p) || p < 0.0 || p >= 1.0 || static_cast<float>(p) >= 1.0f) {
+        throw value_error("p_dropout must be finite and in [0, 1) as float32");
+    }
+    if (!(static_cast<float>(p) > 0.0f)) return a;
+    if (softcap > 0.0) throw value_error("softcap with dropout is not supported by FlashAttention v2");
+    a.keep = 1.0f - static_cast<float>(p);
+    a.threshold = static_cast<uint32_t>(a.keep * 255.0f);
+    a.inv_keep = 1.0f / a.keep;
+    if (d->rng_state) {
+        const kcr_tensor* t = d->rng_state;
+        if (t->dtype != KCR_INT64 || t->ndim != 1 || t->shape[0] != 2 || (t->strides[0] != 1) ||
+            t->device < 0 || t->device != q->device || reinterpret_cast<uintptr_t>(t->data) % 8 != 0) {
+            throw value_error("rng_state must be a contiguous CUDA int64 tensor of shape [2] on q's device");
+        }
+        if (d->offset != 0) throw value_error("offset must be zero when seed is an RNG-state tensor");
+        a.state = static_cast<const int64_t*>(t->data);
+    } else {
+        a.seed = d->seed;
+        a.offset = d->offset;
+    }
+    return a;
+}
+
+template <typename P>
+inline void set_dropout(P& prm, const DropoutArgs& a) {
+    prm.rng_state = a.state;
+    prm.drop_seed = a.seed;
+    prm.drop_offset = a.offset;
+    prm.drop_threshold = a.threshold;
+    prm.inv_keep = a.inv_keep;
 }
 
 inline const char* dtype_name(int dtype) {
@@ -286,6 +336,100 @@ struct TileLane {
         return u32x4{lo.x, lo.y, hi.x, hi.y};
     }
 };
+
+// ---------------------------------------------------------------------------
+// Dropout: FlashAttention-2's Philox4x32-7 stream (flash-attn2-rs/src/device/
+// dropout.rs:31-51). Element (query q, key k) of head bh = b * H + h is kept when
+// byte ((q % 16) / 8 * 2 + k % 2) of word (k % 32) / 8 of
+//     philox(seed, offset + 32 bh + 4 (q % 8) + (k % 8) / 2, row q / 16, col k / 32)
+// is <= threshold (= floor(keep * 255)); rows and columns count from the start
+// of the (varlen) sequence. The mapping is the reference's, fixed by its CUDA
+// fragment layout; the kernels here evaluate it in their own layouts.
+// ---------------------------------------------------------------------------
+struct DropoutState {
+    uint64_t seed;
+    uint64_t offset;
+    uint32_t threshold;
+};
+
+// Seed and offset from the device state tensor when given (read on the launch
+// stream, so a captured graph replays the live values), else from the launch.
+template <typename P>
+__device__ __forceinline__ DropoutState dropout_state(const P& p) {
+    DropoutState d;
+    d.seed = p.rng_state ? static_cast<uint64_t>(p.rng_state[0]) : p.drop_seed;
+    d.offset = p.rng_state ? static_cast<uint64_t>(p.rng_state[1]) : p.drop_offset;
+    d.threshold = p.drop_threshold;
+    return d;
+}
+
+__device__ __forceinline__ void philox4x32_7(uint64_t seed, uint64_t counter, uint32_t row, uint32_t col,
+                                             uint32_t (&out)[4]) {
+    uint32_t c0 = static_cast<uint32_t>(counter), c1 = static_cast<uint32_t>(counter >> 32);
+    uint32_t c2 = row, c3 = col;
+    uint32_t k0 = static_cast<uint32_t>(seed), k1 = static_cast<uint32_t>(seed >> 32);
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+        const uint64_t a = static_cast<uint64_t>(c0) * 0xD2511F53u;
+        const uint64_t b = static_cast<uint64_t>(c2) * 0xCD9E8D57u;
+        const uint32_t n0 = static_cast<uint32_t>(b >> 32) ^ c1 ^ k0;
+        const uint32_t n2 = static_cast<uint32_t>(a >> 32) ^ c3 ^ k1;
+        c1 = static_cast<uint32_t>(b);
+        c3 = static_cast<uint32_t>(a);
+        c0 = n0;
+        c2 = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+// Keep bits for a lane that owns query q and, of the 32-key block kblock, the
+// 16 keys 8 (r / 4) + 4 hh + r % 4 (r = 0..15; the S^T accumulator layout of the
+// forward and dQ kernels). Bit r set = kept.
+__device__ __forceinline__ uint32_t keep_bits_query_lane(const DropoutState& d, uint32_t bh, uint32_t q,
+                                                         uint32_t kblock, int hh) {
+    const uint64_t base = d.offset + 32ull * bh + 4u * (q % 8u) + 2u * hh;
+    uint32_t x0[4], x1[4];
+    philox4x32_7(d.seed, base, q / 16u, kblock, x0);
+    philox4x32_7(d.seed, base + 1, q / 16u, kblock, x1);
+    const uint32_t rshift = ((q % 16u) / 8u) * 16u;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t word = ((r & 3) >> 1) ? x1[r >> 2] : x0[r >> 2];
+        const uint32_t byte = (word >> (rshift + 8u * (r & 1))) & 255u;
+        bits |= (byte <= d.threshold ? 1u : 0u) << r;
+    }
+    return bits;
+}
+
+// Keep bits for a lane that owns key k and the 16 queries q0 + 8 (r / 4) + 4 hh +
+// r % 4 of a 32-row chunk starting at q0 (a multiple of 16; the S = Q K^T
+// accumulator layout of the dK/dV kernels). Bit r set = kept.
+__device__ __forceinline__ uint32_t keep_bits_key_lane(const DropoutState& d, uint32_t bh, uint32_t q0,
+                                                       uint32_t k, int hh) {
+    const uint32_t word = (k % 32u) / 8u;
+    const uint32_t kshift = 8u * (k & 1u);
+    uint32_t bits = 0;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t lane = 4u * (4u * hh + m) + (k % 8u) / 2u;
+            uint32_t x[4];
+            philox4x32_7(d.seed, d.offset + 32ull * bh + lane, q0 / 16u + rb, k / 32u, x);
+            const uint32_t w = word == 0 ? x[0] : word == 1 ? x[1] : word == 2 ? x[2] : x[3];
+            // r = 8 rb + m: query row % 16 = 4 hh + m (< 8); r = 8 rb + 4 + m: + 8.
+            bits |= (((w >> kshift) & 255u) <= d.threshold ? 1u : 0u) << (8 * rb + m);
+            bits |= (((w >> (16u + kshift)) & 255u) <= d.threshold ? 1u : 0u) << (8 * rb + 4 + m);
+        }
+    }
+    return bits;
+}
 
 }  // namespace attn
 }  // namespace kcr

@@ -57,7 +57,11 @@ struct BwdParams {
     float scale_log2;
     float tanh_scale;
     float scale_eff_log2;
-    float grad_scale;  // softmax scale (chain rule through raw scores)
+    float grad_scale;  // softmax scale (chain rule through raw scores) / keep
+    const int64_t* rng_state;  // dropout: device [seed, offset], or null (fields below)
+    uint64_t drop_seed, drop_offset;
+    uint32_t drop_threshold;   // 255 = no dropout
+    float inv_keep;            // dV scale: 1 / keep
 };
 
 // Sequence bounds of batch entry b (dense: the whole tensor).
@@ -208,6 +212,7 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dkv_kernel(const BwdParams 
     const int b = bkv / p.kv_heads;
     const int kvh = bkv - b * p.kv_heads;
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
+    const DropoutState drop = p.drop_threshold < 255 ? dropout_state(p) : DropoutState{};
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
     const int key0 = kbi * BK;
@@ -321,6 +326,11 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dkv_kernel(const BwdParams 
                     dp = mfma32<T>(da, vf[ks], dp);
                 }
                 float pv[16], dsv[16];
+                const uint32_t keep_bits =
+                    p.drop_threshold < 255
+                        ? keep_bits_key_lane(drop, static_cast<uint32_t>(b * p.heads + head),
+                                             static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh)
+                        : 0xFFFFu;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int qloc = 32 * qc + 8 * g + 4 * hh;
@@ -336,8 +346,9 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dkv_kernel(const BwdParams 
                         const float x = bwd_score<GENERAL>(p, s[r], row, my_key, off, slope_log2, dfac);
                         float pr = fast_exp2(x - lsev[e]);
                         if (need_mask && masked_at(row, my_key, sk, off, wl, wr)) pr = 0.0f;
-                        pv[r] = pr;
-                        dsv[r] = pr * (dp[r] - dlv[e]) * dfac;
+                        const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                        pv[r] = kept ? pr : 0.0f;
+                        dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dlv[e]) * dfac;
                     }
                 }
 #pragma unroll
@@ -384,8 +395,8 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dkv_kernel(const BwdParams 
                     uint2 a, c;
                     a.x = pack2<T>(dk[db][4 * g] * gs, dk[db][4 * g + 1] * gs);
                     a.y = pack2<T>(dk[db][4 * g + 2] * gs, dk[db][4 * g + 3] * gs);
-                    c.x = pack2<T>(dv[db][4 * g], dv[db][4 * g + 1]);
-                    c.y = pack2<T>(dv[db][4 * g + 2], dv[db][4 * g + 3]);
+                    c.x = pack2<T>(dv[db][4 * g] * p.inv_keep, dv[db][4 * g + 1] * p.inv_keep);
+                    c.y = pack2<T>(dv[db][4 * g + 2] * p.inv_keep, dv[db][4 * g + 3] * p.inv_keep);
                     *reinterpret_cast<uint2*>(dkrow + d) = a;
                     *reinterpret_cast<uint2*>(dvrow + d) = c;
                 }
@@ -425,6 +436,7 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
     const int kvh = head / p.gqa;
     const int qbi = per - 1 - qo;  // longest causal tiles first
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
+    const DropoutState drop = p.drop_threshold < 255 ? dropout_state(p) : DropoutState{};
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
     const int row0 = qbi * BM;
@@ -521,6 +533,11 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             float dsv[16];
+            const uint32_t keep_bits =
+                p.drop_threshold < 255
+                    ? keep_bits_query_lane(drop, static_cast<uint32_t>(b * p.heads + head),
+                                           static_cast<uint32_t>(my_row), static_cast<uint32_t>(kb / 32 + sub), hh)
+                    : 0xFFFFu;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -528,7 +545,8 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
                 const float x = bwd_score<GENERAL>(p, s[sub][r], my_row, col, off, slope_log2, dfac);
                 float pr = fast_exp2(x - lse2);
                 if (need_mask && masked_at(my_row, col, sk, off, wl, wr)) pr = 0.0f;
-                dsv[r] = pr * (dp[sub][r] - dlt) * dfac;
+                const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                dsv[r] = pr * ((kept ? dp[sub][r] : 0.0f) - dlt) * dfac;
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -579,7 +597,7 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 // Two LDS stages, one barrier per tile; 2 waves per SIMD.
 // ---------------------------------------------------------------------------
 
-template <typename T, int D, int NW, bool VARLEN>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {
     constexpr int BN = 64;
     constexpr int BM = 32 * NW;
@@ -620,6 +638,9 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
         head = kvh * p.gqa + idx / nbkv;
     }
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
+    DropoutState drop{};
+    if constexpr (DROPOUT) drop = dropout_state(p);
+    const uint32_t bh = static_cast<uint32_t>(b * p.heads + head);
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
     // Counted from the end of this sequence (varlen sequences end at different tiles).
@@ -697,6 +718,11 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             float dsv[16];
+            uint32_t keep_bits = 0xFFFFu;
+            if constexpr (DROPOUT) {
+                keep_bits = keep_bits_query_lane(drop, bh, static_cast<uint32_t>(my_row),
+                                                 static_cast<uint32_t>(kb / 32 + sub), hh);
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float pr = fast_exp2(__builtin_fmaf(s[sub][r], c, -lse2));
@@ -706,7 +732,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
                                         (wl >= 0 & col < my_row + off - wl);
                     pr = masked ? 0.0f : pr;
                 }
-                dsv[r] = pr * (dp[sub][r] - dlt);
+                dsv[r] = pr * ((((keep_bits >> r) & 1u) ? dp[sub][r] : 0.0f) - dlt);
             }
 #pragma unroll
             for (int t2 = 0; t2 < 2; ++t2) {
@@ -744,7 +770,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     }
 }
 
-template <typename T, int D, int NW, bool VARLEN>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const BwdParams p) {
     // D = 128: the dK and dV accumulators (128 registers) and K (32) leave no
     // room for V in registers at 2 waves per SIMD, so V is staged once in LDS
@@ -787,6 +813,8 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
         kvh = bkv - b * p.kv_heads;
     }
     const SeqBounds sb = seq_bounds<VARLEN>(p, b);
+    DropoutState drop{};
+    if constexpr (DROPOUT) drop = dropout_state(p);
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
     const int key0 = kbi * BK;
@@ -886,6 +914,11 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
             }
             u32x4 pP[2], pS[2];
             float pv[16], dsv[16];
+            uint32_t keep_bits = 0xFFFFu;
+            if constexpr (DROPOUT) {
+                keep_bits = keep_bits_key_lane(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + (t % gqa)),
+                                               static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh);
+            }
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int qloc = 32 * qc + 8 * g + 4 * hh;
@@ -903,8 +936,9 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                                             (wl >= 0 & my_key < row + off - wl);
                         pr = masked ? 0.0f : pr;
                     }
-                    pv[r] = pr;
-                    dsv[r] = pr * (dp[r] - dv4[e]);
+                    const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                    pv[r] = kept ? pr : 0.0f;
+                    dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
                 }
             }
 #pragma unroll
@@ -944,8 +978,8 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                 uint2 a, cc;
                 a.x = pack2<T>(dk[db][4 * g] * gs, dk[db][4 * g + 1] * gs);
                 a.y = pack2<T>(dk[db][4 * g + 2] * gs, dk[db][4 * g + 3] * gs);
-                cc.x = pack2<T>(dv[db][4 * g], dv[db][4 * g + 1]);
-                cc.y = pack2<T>(dv[db][4 * g + 2], dv[db][4 * g + 3]);
+                cc.x = pack2<T>(dv[db][4 * g] * p.inv_keep, dv[db][4 * g + 1] * p.inv_keep);
+                cc.y = pack2<T>(dv[db][4 * g + 2] * p.inv_keep, dv[db][4 * g + 3] * p.inv_keep);
                 *reinterpret_cast<uint2*>(dkrow + d) = a;
                 *reinterpret_cast<uint2*>(dvrow + d) = cc;
             }
@@ -983,14 +1017,14 @@ void zero_f32(float* x, int64_t n, hipStream_t s) {
     check_launch("zero delta");
 }
 
-template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES>
+template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES, bool DROPOUT>
 void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
     if (want_kv) {
         constexpr int BK = 32 * DKV_WAVES;
         prm.blocks_per_seq = (prm.seqlen_k + BK - 1) / BK;
         const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.kv_heads;
         if (blocks > 0) {
-            flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN><<<static_cast<unsigned>(blocks), DKV_WAVES * 64, 0, s>>>(prm);
+            flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN, DROPOUT><<<static_cast<unsigned>(blocks), DKV_WAVES * 64, 0, s>>>(prm);
             check_launch("launch flash_bwd_dkv");
         }
     }
@@ -999,7 +1033,7 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
         prm.blocks_per_seq = (prm.seqlen_q + BM - 1) / BM;
         const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.heads;
         if (blocks > 0) {
-            flash_bwd_dq_v2_kernel<T, D, DQ_WAVES, VARLEN><<<static_cast<unsigned>(blocks), DQ_WAVES * 64, 0, s>>>(prm);
+            flash_bwd_dq_v2_kernel<T, D, DQ_WAVES, VARLEN, DROPOUT><<<static_cast<unsigned>(blocks), DQ_WAVES * 64, 0, s>>>(prm);
             check_launch("launch flash_bwd_dq");
         }
     }
@@ -1018,7 +1052,11 @@ void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
             // concurrent blocks then share one sequence's tiles in L2. Masked
             // dense grids keep the tile-major, longest-first order.
             prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
-            launch_bwd_v2<T, D, VARLEN, 4, 4>(prm, want_q, want_kv, s);
+            if (prm.drop_threshold < 255) {
+                launch_bwd_v2<T, D, VARLEN, 4, 4, true>(prm, want_q, want_kv, s);
+            } else {
+                launch_bwd_v2<T, D, VARLEN, 4, 4, false>(prm, want_q, want_kv, s);
+            }
             return;
         }
     }
@@ -1108,14 +1146,17 @@ void check_alibi_shape(const kcr_tensor* alibi, int64_t b, int64_t h, int32_t& a
     require_device(alibi, "alibi");
 }
 
-void fill_common(BwdParams& prm, const Options& opt, double scale_used) {
+// gradient_scale = scale / keep (host/backward.rs:159-160): dS is formed with the
+// masked dP and the keep-scaled delta, so its 1 / keep rides on dQ and dK.
+void fill_common(BwdParams& prm, const Options& opt, double scale_used, const DropoutArgs& drop) {
+    set_dropout(prm, drop);
     prm.window_left = opt.window_left;
     prm.window_right = opt.window_right;
     prm.alibi_causal = opt.alibi_causal;
     prm.scale_log2 = opt.scale * kLog2e;
     prm.tanh_scale = opt.tanh_scale;
     prm.scale_eff_log2 = opt.scale_eff * kLog2e;
-    prm.grad_scale = static_cast<float>(scale_used);
+    prm.grad_scale = static_cast<float>(scale_used) / drop.keep;
 }
 
 }  // namespace
@@ -1169,7 +1210,7 @@ extern "C" int64_t kcr_flash_bwd_workspace_bytes(int64_t, int64_t, int64_t, int6
 extern "C" int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                              const kcr_tensor* dout, const kcr_tensor* lse, const kcr_tensor* delta,
                              const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                             int64_t window_left, int64_t window_right, double softcap,
+                             int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                              const kcr_tensor* dq, const kcr_tensor* dk, const kcr_tensor* dv,
                              void* workspace, int64_t workspace_bytes, void* stream) {
     (void)workspace;
@@ -1208,6 +1249,7 @@ extern "C" int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         auto s = static_cast<hipStream_t>(stream);
         const double scale_used = has_scale ? scale : 1.0 / std::sqrt(static_cast<double>(D));
         const Options opt = normalize_options(has_scale, scale, causal, window_left, window_right, softcap, D, Sk);
+        const DropoutArgs drop = parse_dropout(dropout, softcap, q);
         if (Sq == 0 || Sk == 0) {
             if (dq) zero_u16(dq->data, numel(*dq), s);
             if (dk) zero_u16(dk->data, numel(*dk), s);
@@ -1239,7 +1281,7 @@ extern "C" int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         prm.seqlen_k = static_cast<int32_t>(Sk);
         prm.head_dim = static_cast<int32_t>(D);
         prm.alibi_b = alibi_b;
-        fill_common(prm, opt, scale_used);
+        fill_common(prm, opt, scale_used, drop);
         const int bucket = static_cast<int>((D + 31) / 32 * 32);
         launch_bwd<false>(prm, q->dtype, bucket, opt.tanh_scale > 0.0f || alibi, dq != nullptr, dk != nullptr, s);
     });
@@ -1251,7 +1293,7 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
                                     const kcr_tensor* dout, const kcr_tensor* out, const kcr_tensor* lse,
                                     const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
                                     const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                                    int64_t window_left, int64_t window_right, double softcap,
+                                    int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                                     int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
                                     const kcr_tensor* dq, const kcr_tensor* dk, const kcr_tensor* dv,
                                     const kcr_tensor* delta, void* workspace, int64_t workspace_bytes,
@@ -1305,6 +1347,7 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
         if (max_seqlen_q == 1 && !alibi) causal_eff = 0;
         const Options opt = normalize_options(has_scale, scale, causal_eff, window_left, window_right, softcap,
                                               D, max_seqlen_k);
+        const DropoutArgs drop = parse_dropout(dropout, softcap, q);
         // Gradients of keys no query sees, rows of empty sequences and the delta
         // padding are defined as zero.
         zero_u16(dq->data, numel(*dq), s);
@@ -1322,7 +1365,7 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
                 static_cast<float*>(delta->data), static_cast<const int32_t*>(cu_seqlens_q->data), 0,
                 dout->strides[0], dout->strides[1], 0, out->strides[0], out->strides[1], 0,
                 Tq + 128 * batch, static_cast<int>(max_seqlen_q), static_cast<int>(rounded),
-                static_cast<int>(H), static_cast<int>(D), lanes, 1.0f, Tq);
+                static_cast<int>(H), static_cast<int>(D), lanes, drop.keep, Tq);
         };
         if (q->dtype == KCR_BFLOAT16) go(bf16_t{}); else go(f16_t{});
         check_launch("launch varlen preprocess");
@@ -1353,7 +1396,7 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
         prm.seqlen_k = static_cast<int32_t>(max_seqlen_k);
         prm.head_dim = static_cast<int32_t>(D);
         prm.alibi_b = alibi_b;
-        fill_common(prm, opt, scale_used);
+        fill_common(prm, opt, scale_used, drop);
         const int bucket = static_cast<int>((D + 31) / 32 * 32);
         launch_bwd<true>(prm, q->dtype, bucket, opt.tanh_scale > 0.0f || alibi, true, true, s);
     });

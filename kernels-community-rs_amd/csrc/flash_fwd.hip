@@ -95,6 +95,7 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     const int b = bh / p.heads;
     const int head = bh - b * p.heads;
     const int kvh = head / p.gqa;
+    const DropoutState drop = p.drop_threshold < 255 ? dropout_state(p) : DropoutState{};
     // Longest causal tiles first: block qo takes the qo-th query tile counted
     // from the end of its own sequence (varlen sequences end at different tiles).
     int qb = p.q_blocks - 1 - qo;
@@ -371,6 +372,17 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
                 }
             }
             l[qt] += rowsum;
+            if (p.drop_threshold < 255) {
+                // Dropout after the (undropped) row sum: P and O only.
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub) {
+                    const uint32_t bits = keep_bits_query_lane(drop, static_cast<uint32_t>(bh),
+                                                               static_cast<uint32_t>(row),
+                                                               static_cast<uint32_t>(kb / 32 + sub), hh);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[qt][sub][r] = ((bits >> r) & 1u) ? s[qt][sub][r] : 0.0f;
+                }
+            }
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
                 const int sub = tt >> 1;
@@ -405,7 +417,7 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
         const int row = wrow0 + qt * 32 + l32;
         const float lt = l[qt] + __shfl_xor(l[qt], 32, 64);
         if (row >= sq) continue;
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const float inv = (lt > 0.0f ? 1.0f / lt : 0.0f) * (p.drop_threshold < 255 ? p.inv_keep : 1.0f);
         uint16_t* orow = obase + row * p.o_s;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -436,7 +448,7 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // packed in place into the B operand of the PV MFMA. Two LDS stages, the next
 // tile's copy in flight during the current tile, one barrier per tile.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool VARLEN>
+template <typename T, int D, bool VARLEN, bool DROPOUT>
 __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams p) {
     constexpr int NW = 4;
     constexpr int BN = kBN;
@@ -486,6 +498,9 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         head = bh - b * p.heads;
     }
     const int kvh = head / p.gqa;
+    const uint32_t bh = static_cast<uint32_t>(b * p.heads + head);
+    DropoutState drop{};
+    if constexpr (DROPOUT) drop = dropout_state(p);
     // Block qo takes the qo-th query tile counted from the end of its sequence
     // (varlen sequences end at different tiles).
     int qb = p.q_blocks - 1 - qo;
@@ -627,6 +642,17 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
             }
         }
         l += rowsum;
+        if constexpr (DROPOUT) {
+            // The row sum above is of the undropped probabilities; dropped ones
+            // leave P (and O) only.
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+                const uint32_t bits = keep_bits_query_lane(drop, bh, static_cast<uint32_t>(row),
+                                                           static_cast<uint32_t>(kb / 32 + sub), hh);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[sub][r] = ((bits >> r) & 1u) ? s[sub][r] : 0.0f;
+            }
+        }
         // P^T packed in place: k-slot j of group tt is key 16tt + 8(j/4) + 4hh + j%4.
         u32x4 pk[4];
 #pragma unroll
@@ -648,7 +674,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
 
     const float lt = l + __shfl_xor(l, 32, 64);
     if (row < sq) {
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const float inv = (lt > 0.0f ? 1.0f / lt : 0.0f) * (DROPOUT ? p.inv_keep : 1.0f);
         uint16_t* orow = obase + row * p.o_s;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -743,7 +769,11 @@ void launch_tiled(FwdParams& prm, hipStream_t s) {
     // Sequence-major order for packed sequences and unmasked grids (blocks of
     // equal work); masked dense grids keep the longest-first tile-major order.
     prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
-    flash_fwd_tiled_kernel<T, D, VARLEN><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+    if (prm.drop_threshold < 255) {
+        flash_fwd_tiled_kernel<T, D, VARLEN, true><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+    } else {
+        flash_fwd_tiled_kernel<T, D, VARLEN, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+    }
     check_launch("launch flash_fwd");
 }
 
@@ -826,7 +856,7 @@ using namespace kcr::attn;
 
 extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                              const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                             int64_t window_left, int64_t window_right, double softcap,
+                             int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                              const kcr_tensor* out, const kcr_tensor* lse, void* stream) {
     return guarded([&] {
         check_qkv(q, "q", 4);
@@ -877,6 +907,7 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         auto s = static_cast<hipStream_t>(stream);
         const Options opt = normalize_options(has_scale, scale, causal, window_left, window_right,
                                               softcap, D, Sk);
+        const DropoutArgs drop = parse_dropout(dropout, softcap, q);
         if (Sq == 0) return;
         if (Sk == 0) {
             // Every row is empty: O = 0, LSE = +inf.
@@ -916,6 +947,7 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         prm.scale_log2 = opt.scale * kLog2e;
         prm.tanh_scale = opt.tanh_scale;
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
+        set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<false>(prm, q->dtype, bucket_for(D), general, s);
     });
@@ -926,7 +958,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
                                     const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
                                     const kcr_tensor* alibi, int has_scale, double scale,
                                     int causal, int64_t window_left, int64_t window_right,
-                                    double softcap, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                    double softcap, const kcr_dropout* dropout, int64_t max_seqlen_q, int64_t max_seqlen_k,
                                     int zero_tensors, const kcr_tensor* out,
                                     const kcr_tensor* lse, void* stream) {
     return guarded([&] {
@@ -987,6 +1019,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         if (max_seqlen_q == 1 && !alibi) causal_eff = 0;
         const Options opt = normalize_options(has_scale, scale, causal_eff, window_left, window_right,
                                               softcap, D, max_seqlen_k);
+        const DropoutArgs drop = parse_dropout(dropout, softcap, q);
         if (zero_tensors || max_seqlen_k == 0) {
             // varlen/mod.rs:418-443: cleared output, LSE -inf (+inf without keys).
             zero_rows(out->data, Tq, H * D, out->strides[0], s);
@@ -1026,6 +1059,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         prm.scale_log2 = opt.scale * kLog2e;
         prm.tanh_scale = opt.tanh_scale;
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
+        set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<true>(prm, q->dtype, bucket_for(D), general, s);
     });

@@ -18,8 +18,10 @@ positional signatures and return conventions, backed by libkcr_hip.so.
 Outputs the reference allocates with `TVMFFIEnvTensorAlloc` are allocated here with
 torch's allocator (the same allocator tvm-ffi forwards to under torch). Inputs
 whose rows are not 16-byte aligned are repacked first, as the reference does
-with `copy_attention_layout` (host/layout.rs:46-125). Dropout (p > 0) is not part
-of this build.
+with `copy_attention_layout` (host/layout.rs:46-125). Dropout follows the
+reference's Philox4x32-7 mask stream, keyed by explicit (seed, offset) or by a
+device int64 [2] RNG-state tensor; diagnostic probabilities (return_softmax) and
+the generator-descriptor arities are not part of this build.
 """
 
 from __future__ import annotations
@@ -27,9 +29,10 @@ from __future__ import annotations
 import ctypes
 from types import SimpleNamespace
 
+import numpy as np
 import torch
 
-from kcr_native import call, describe, lib, op_namespace_prefixer, ref, stream_of
+from kcr_native import call, describe, dropout_arg, lib, op_namespace_prefixer, ref, stream_of
 
 torch_add_op_namespace_prefix = op_namespace_prefixer("flash_attn2")
 
@@ -51,12 +54,17 @@ def _packed(t):
     return t.clone(memory_format=torch.contiguous_format)
 
 
-def _no_dropout(p):
+def _dropout_p(p):
     p = float(p)
-    if not (p == p) or not 0.0 <= p < 1.0:
+    if not (p == p) or not 0.0 <= p < 1.0 or float(np.float32(p)) >= 1.0:
         raise ValueError("p_dropout must be finite and in [0, 1) as float32")
-    if p > 0.0:
-        raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
+    return p
+
+
+def _rng_state_ok(state, q):
+    return (isinstance(state, torch.Tensor) and state.is_cuda and state.device == q.device
+            and state.dtype == torch.int64 and state.shape == (2,) and state.is_contiguous()
+            and state.data_ptr() % 8 == 0)
 
 
 def _scale_args(scale):
@@ -65,6 +73,10 @@ def _scale_args(scale):
 
 def _fwd_impl(args, lse_only):
     n = len(args)
+    if n in (14, 16, 18):
+        raise NotImplementedError(
+            "diagnostic probabilities and generator descriptors (fwd arities 14/16/18) are not "
+            "part of this build")
     if n not in (9, 10, 12, 13):
         raise ValueError(
             "fwd expects 9 positional arguments (q, k, v, alibi_slopes, softmax_scale, "
@@ -72,8 +84,14 @@ def _fwd_impl(args, lse_only):
             f"p_dropout, seed, offset, and/or an output tensor; got {n}"
         )
     q, k, v, alibi, scale, causal, wl, wr, softcap = args[:9]
+    p, seed, offset, state = 0.0, 0, 0, None
     if n >= 12:
-        _no_dropout(args[9])
+        p = _dropout_p(args[9])
+        if isinstance(args[10], torch.Tensor):
+            state = args[10]
+        else:
+            seed = int(args[10])
+        offset = int(args[11])
     supplied = args[-1] if n in (10, 13) else None
     if lse_only and supplied is None:
         raise ValueError("LSE-only forward requires a supplied output")
@@ -92,8 +110,9 @@ def _fwd_impl(args, lse_only):
     lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
     has_scale, sc = _scale_args(scale)
     descs = [describe(t) for t in (qp, kp, vp, alibi)]
+    keep_alive, drop = dropout_arg(p, seed, offset, state)
     call("kcr_flash_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
-         ctypes.c_int64(int(wl)), ctypes.c_int64(int(wr)), ctypes.c_double(float(softcap)),
+         ctypes.c_int64(int(wl)), ctypes.c_int64(int(wr)), ctypes.c_double(float(softcap)), drop,
          ref(describe(out)), ref(describe(lse)), stream_of(q))
     if copy_out:
         supplied.copy_(out)
@@ -114,16 +133,27 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
                         zero_tensors, block_table=None):
     if block_table is not None:
         raise NotImplementedError("paged K/V (block_table) is not supported by this build")
-    _no_dropout(p)
+    # host/varlen/mod.rs:201-229
+    p = float(p)
+    if (not (p == p) or not 0.0 <= p < 1.0 or float(np.float32(p)) >= 1.0
+            or (float(np.float32(p)) > 0.0 and float(softcap) > 0.0)
+            or (return_softmax and float(np.float32(p)) == 0.0)):
+        raise ValueError("invalid dropout, softcap, or probability request")
     if return_softmax:
-        raise ValueError("return_softmax requires nonzero dropout and a CUDA RNG-state tensor")
+        raise NotImplementedError("diagnostic probabilities (return_softmax) are not part of this build")
+    if float(np.float32(p)) > 0.0:
+        if state is None:
+            raise ValueError("dropout requires RNG state")
+        if not _rng_state_ok(state, q):
+            raise ValueError("RNG state must be contiguous int64 [2] on q's device")
     qp, kp, vp = _packed(q), _packed(k), _packed(v)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
     has_scale, sc = _scale_args(scale)
     descs = [describe(t) for t in (qp, kp, vp, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi)]
+    keep_alive, drop = dropout_arg(p, 0, 0, state)
     call("kcr_flash_varlen_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
-         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)),
+         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)), drop,
          ctypes.c_int64(int(max_q)), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)),
          ref(describe(out)), ref(describe(lse)), stream_of(q))
     probabilities = torch.empty(0, dtype=q.dtype, device=q.device)
@@ -131,7 +161,9 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
 
 
 def bwd_preprocess(dout, out, p):
-    _no_dropout(p)
+    p = float(p)
+    if not (p == p) or not 0.0 <= p < 1.0 or float(np.float32(p)) >= 1.0:
+        raise ValueError("p_dropout must be in [0, 1) as float32")
     if out.ndim != 4 or dout.shape != out.shape:
         raise ValueError("dout and out must share shape, dtype and device")
     b, s, h, d = out.shape
@@ -148,8 +180,17 @@ def _bwd(args, want_q, want_kv):
             "backward component expects q, k, v, dout, lse, delta, alibi, scale, causal, left, "
             "right, softcap, dropout, rng_state"
         )
-    q, k, v, dout, lse, delta, alibi, scale, causal, left, right, softcap, p, _state = args
-    _no_dropout(p)
+    q, k, v, dout, lse, delta, alibi, scale, causal, left, right, softcap, p, rng = args
+    p = float(p)
+    # host/backward.rs:75-113
+    if (not (p == p) or not 0.0 <= p < 1.0 or float(np.float32(p)) >= 1.0
+            or (float(np.float32(p)) > 0.0 and float(softcap) > 0.0)):
+        raise ValueError("invalid dropout or dropout combined with softcap")
+    if float(np.float32(p)) > 0.0:
+        if rng is None:
+            raise ValueError("dropout backward requires saved RNG state")
+        if not _rng_state_ok(rng, q):
+            raise ValueError("RNG state must be contiguous CUDA int64 [2] on q's device")
     qp, kp, vp, dp = _packed(q), _packed(k), _packed(v), _packed(dout)
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device) if want_q else None
     dk = torch.empty(k.shape, dtype=k.dtype, device=k.device) if want_kv else None
@@ -159,8 +200,9 @@ def _bwd(args, want_q, want_kv):
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     has_scale, sc = _scale_args(scale)
     descs = [describe(t) for t in (qp, kp, vp, dp, lse, delta, alibi)]
+    keep_alive, drop = dropout_arg(p, 0, 0, rng)
     call("kcr_flash_bwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
-         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)),
+         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)), drop,
          ref(describe(dq)), ref(describe(dk)), ref(describe(dv)),
          ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), stream_of(q))
     return dq, dk, dv
@@ -181,7 +223,15 @@ def bwd_all(*args):
 
 def varlen_bwd_explicit(q, k, v, dout, out, lse, cu_seqlens_q, cu_seqlens_k, alibi, scale, causal,
                         left, right, softcap, p, state, max_q, max_k, zero_tensors):
-    _no_dropout(p)
+    p = float(p)
+    if (not (p == p) or not 0.0 <= p < 1.0 or float(np.float32(p)) >= 1.0
+            or (float(np.float32(p)) > 0.0 and float(softcap) > 0.0)):
+        raise ValueError("invalid dropout or dropout combined with softcap")
+    if float(np.float32(p)) > 0.0:
+        if state is None:
+            raise ValueError("dropout backward requires saved RNG state")
+        if not _rng_state_ok(state, q):
+            raise ValueError("RNG state must be contiguous CUDA int64 [2] on q's device")
     qp, kp, vp, dp, op = (_packed(t) for t in (q, k, v, dout, out))
     batch = cu_seqlens_q.numel() - 1
     tq, h, d = q.shape
@@ -193,8 +243,9 @@ def varlen_bwd_explicit(q, k, v, dout, out, lse, cu_seqlens_q, cu_seqlens_k, ali
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     has_scale, sc = _scale_args(scale)
     descs = [describe(t) for t in (qp, kp, vp, dp, op, lse, cu_seqlens_q, cu_seqlens_k, alibi)]
+    keep_alive, drop = dropout_arg(p, 0, 0, state)
     call("kcr_flash_varlen_bwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
-         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)),
+         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)), drop,
          ctypes.c_int64(int(max_q)), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)),
          ref(describe(dq)), ref(describe(dk)), ref(describe(dv)), ref(describe(delta)),
          ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), stream_of(q))

@@ -20,32 +20,37 @@ def _custom_op(name):
 
 @_custom_op("_dense_forward")
 def _dense_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
-                   left: int, right: int, softcap: float,
-                   slopes: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
-    out, lse, _, _ = fwd(q, k, v, alibi_slopes=slopes, softmax_scale=scale, is_causal=causal,
-                         window_size_left=left, window_size_right=right, softcap=softcap)
-    return out, lse
+                   left: int, right: int, softcap: float, slopes: Optional[torch.Tensor],
+                   dropout_p: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    out, lse, _, rng_state = fwd(q, k, v, alibi_slopes=slopes, p_dropout=dropout_p, softmax_scale=scale,
+                                 is_causal=causal, window_size_left=left, window_size_right=right,
+                                 softcap=softcap)
+    return out, lse, rng_state
 
 
 @_dense_forward.register_fake
-def _(q, k, v, scale, causal, left, right, softcap, slopes):
+def _(q, k, v, scale, causal, left, right, softcap, slopes, dropout_p):
     b, sq, h, _ = q.shape
-    return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
+    return (torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32),
+            q.new_empty((2,), dtype=torch.int64))
 
 
 @_custom_op("_dense_backward")
 def _dense_backward(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     out: torch.Tensor, lse: torch.Tensor, scale: float, causal: bool, left: int,
                     right: int, softcap: float, slopes: Optional[torch.Tensor],
-                    deterministic: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    dq, dk, dv, _ = bwd(dout, q, k, v, out, lse, alibi_slopes=slopes, softmax_scale=scale,
-                        is_causal=causal, window_size_left=left, window_size_right=right,
-                        softcap=softcap, deterministic=deterministic)
+                    deterministic: bool, dropout_p: float,
+                    rng_state: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dq, dk, dv, _ = bwd(dout, q, k, v, out, lse, alibi_slopes=slopes, p_dropout=dropout_p,
+                        softmax_scale=scale, is_causal=causal, window_size_left=left,
+                        window_size_right=right, softcap=softcap, deterministic=deterministic,
+                        rng_state=rng_state)
     return dq, dk, dv
 
 
 @_dense_backward.register_fake
-def _(dout, q, k, v, out, lse, scale, causal, left, right, softcap, slopes, deterministic):
+def _(dout, q, k, v, out, lse, scale, causal, left, right, softcap, slopes, deterministic, dropout_p,
+      rng_state):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
@@ -69,18 +74,17 @@ class _DenseAttention(torch.autograd.Function):
             k, v = k.unbind(2)
         if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
             raise ValueError("q, k, v must have shape [B, S, H, D]")
-        if dropout_p:
-            raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
         dim = q.shape[-1]
         if not 0 < dim <= 256:
             raise ValueError("head size must be in 1..256")
         scale = dim ** -0.5 if softmax_scale is None else float(softmax_scale)
         q, k, v = _pad(dim, q, k, v)
         left, right = window_size
-        out, lse = _dense_forward(q, k, v, scale, bool(causal), int(left), int(right),
-                                  float(softcap), alibi_slopes)
-        ctx.save_for_backward(q, k, v, out, lse, alibi_slopes)
-        ctx.options = (scale, bool(causal), int(left), int(right), float(softcap), bool(deterministic))
+        out, lse, rng_state = _dense_forward(q, k, v, scale, bool(causal), int(left), int(right),
+                                             float(softcap), alibi_slopes, float(dropout_p))
+        ctx.save_for_backward(q, k, v, out, lse, alibi_slopes, rng_state)
+        ctx.options = (scale, bool(causal), int(left), int(right), float(softcap), bool(deterministic),
+                       float(dropout_p))
         ctx.dim, ctx.packing = dim, packing
         out = out[..., :dim]
         if return_attn_probs:
@@ -90,11 +94,12 @@ class _DenseAttention(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, dout, *unused):
-        q, k, v, out, lse, slopes = ctx.saved_tensors
-        scale, causal, left, right, cap, deterministic = ctx.options
+        q, k, v, out, lse, slopes, rng_state = ctx.saved_tensors
+        scale, causal, left, right, cap, deterministic, dropout_p = ctx.options
         (dout,) = _pad(ctx.dim, dout)
         dq, dk, dv = _dense_backward(dout, q, k, v, out, lse, scale, causal, left, right, cap,
-                                     slopes, deterministic)
+                                     slopes, deterministic, dropout_p,
+                                     rng_state if dropout_p > 0 else None)
         dq, dk, dv = (x[..., : ctx.dim] for x in (dq, dk, dv))
         if ctx.packing == 3:
             grads = (torch.stack((dq, dk, dv), dim=2), None, None)
@@ -108,35 +113,38 @@ class _DenseAttention(torch.autograd.Function):
 @_custom_op("_varlen_forward")
 def _varlen_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cuq: torch.Tensor,
                     cuk: torch.Tensor, max_q: int, max_k: int, scale: float, causal: bool,
-                    left: int, right: int, softcap: float,
-                    slopes: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
-    out, lse, _, _ = varlen_fwd(q, k, v, cuq, cuk, max_seqlen_q=max_q, max_seqlen_k=max_k,
-                                softmax_scale=scale, is_causal=causal, window_size_left=left,
-                                window_size_right=right, softcap=softcap, alibi_slopes=slopes)
-    return out, lse
+                    left: int, right: int, softcap: float, slopes: Optional[torch.Tensor],
+                    dropout_p: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    out, lse, _, rng_state = varlen_fwd(q, k, v, cuq, cuk, max_seqlen_q=max_q, max_seqlen_k=max_k,
+                                        p_dropout=dropout_p, softmax_scale=scale, is_causal=causal,
+                                        window_size_left=left, window_size_right=right,
+                                        softcap=softcap, alibi_slopes=slopes)
+    return out, lse, rng_state
 
 
 @_varlen_forward.register_fake
-def _(q, k, v, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes):
+def _(q, k, v, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes, dropout_p):
     total, h, _ = q.shape
-    return torch.empty_like(q), q.new_empty((h, total), dtype=torch.float32)
+    return (torch.empty_like(q), q.new_empty((h, total), dtype=torch.float32),
+            q.new_empty((2,), dtype=torch.int64))
 
 
 @_custom_op("_varlen_backward")
 def _varlen_backward(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      out: torch.Tensor, lse: torch.Tensor, cuq: torch.Tensor, cuk: torch.Tensor,
                      max_q: int, max_k: int, scale: float, causal: bool, left: int, right: int,
-                     softcap: float, slopes: Optional[torch.Tensor]
-                     ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                     softcap: float, slopes: Optional[torch.Tensor], dropout_p: float,
+                     rng_state: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     dq, dk, dv, _ = varlen_bwd(dout, q, k, v, out, lse, cuq, cuk, alibi_slopes=slopes,
-                               max_seqlen_q=max_q, max_seqlen_k=max_k, softmax_scale=scale,
-                               is_causal=causal, window_size_left=left, window_size_right=right,
-                               softcap=softcap)
+                               max_seqlen_q=max_q, max_seqlen_k=max_k, p_dropout=dropout_p,
+                               softmax_scale=scale, is_causal=causal, window_size_left=left,
+                               window_size_right=right, softcap=softcap, rng_state=rng_state)
     return dq, dk, dv
 
 
 @_varlen_backward.register_fake
-def _(dout, q, k, v, out, lse, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes):
+def _(dout, q, k, v, out, lse, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes,
+      dropout_p, rng_state):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
@@ -158,18 +166,18 @@ class _VarlenAttention(torch.autograd.Function):
             k, v = k.unbind(1)
         if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
             raise ValueError("q must be rank 3; k/v must be rank 4 with block_table, otherwise rank 3")
-        if dropout_p:
-            raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
         dim = q.shape[-1]
         if not 0 < dim <= 256:
             raise ValueError("head size must be in 1..256")
         scale = dim ** -0.5 if softmax_scale is None else float(softmax_scale)
         q, k, v = _pad(dim, q, k, v)
         left, right = window_size
-        out, lse = _varlen_forward(q, k, v, cuq, cuk, int(max_q), int(max_k), scale, bool(causal),
-                                   int(left), int(right), float(softcap), slopes)
-        ctx.save_for_backward(q, k, v, out, lse, cuq, cuk, slopes)
-        ctx.options = (int(max_q), int(max_k), scale, bool(causal), int(left), int(right), float(softcap))
+        out, lse, rng_state = _varlen_forward(q, k, v, cuq, cuk, int(max_q), int(max_k), scale,
+                                              bool(causal), int(left), int(right), float(softcap),
+                                              slopes, float(dropout_p))
+        ctx.save_for_backward(q, k, v, out, lse, cuq, cuk, slopes, rng_state)
+        ctx.options = (int(max_q), int(max_k), scale, bool(causal), int(left), int(right), float(softcap),
+                       float(dropout_p))
         ctx.dim, ctx.packing = dim, packing
         out = out[..., :dim]
         if return_probs:
@@ -179,11 +187,12 @@ class _VarlenAttention(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, dout, *unused):
-        q, k, v, out, lse, cuq, cuk, slopes = ctx.saved_tensors
-        max_q, max_k, scale, causal, left, right, cap = ctx.options
+        q, k, v, out, lse, cuq, cuk, slopes, rng_state = ctx.saved_tensors
+        max_q, max_k, scale, causal, left, right, cap, dropout_p = ctx.options
         (dout,) = _pad(ctx.dim, dout)
         dq, dk, dv = _varlen_backward(dout, q, k, v, out, lse, cuq, cuk, max_q, max_k, scale,
-                                      causal, left, right, cap, slopes)
+                                      causal, left, right, cap, slopes, dropout_p,
+                                      rng_state if dropout_p > 0 else None)
         dq, dk, dv = (x[..., : ctx.dim] for x in (dq, dk, dv))
         if ctx.packing == 3:
             grads = (torch.stack((dq, dk, dv), dim=1), None, None)

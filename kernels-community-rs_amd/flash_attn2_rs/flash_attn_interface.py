@@ -8,8 +8,15 @@ flash-attn2-rs/tvm-ffi-ext/flash_attn2_rs/flash_attn_interface.py:
 
 Same argument names, defaults, return lists and error kinds for the validation
 that matters on this path (dtype, device, shapes, head size, GQA divisibility).
-Dropout, paged K/V and the KV-cache entry points are outside this build and
-raise NotImplementedError.
+
+Dropout uses the reference's Philox4x32-7 mask stream keyed by a CUDA int64 [2]
+RNG-state tensor [seed, offset], returned by the forward and passed to the
+backward. The reference reserves those values with
+`torch.Generator.philox_state` (Torch >= 2.14); this build draws them from the
+generator with `torch.randint`, so the stream is reproducible under
+`torch.manual_seed`, and a caller that passes the same [seed, offset] gets the
+reference's masks. Diagnostic probabilities (return_softmax), paged K/V and the
+KV-cache entry points are outside this build and raise NotImplementedError.
 """
 
 from __future__ import annotations
@@ -25,13 +32,29 @@ def _cpu_dispatch(op):
     raise NotImplementedError(f"flash_attn2_rs::{op} has no CPU implementation")
 
 
-def _check_dropout(p):
+def _check_dropout(p, softcap=0.0):
     p = float(p)
     if not math.isfinite(p) or not 0.0 <= p < 1.0:
         raise RuntimeError("p_dropout must be finite and in [0, 1) as float32")
-    if p > 0.0:
-        raise NotImplementedError("dropout (p_dropout > 0) is not supported by this build")
+    if p > 0.0 and float(softcap) > 0.0:
+        raise RuntimeError("Softcapping does not support dropout for now")
     return p
+
+
+def _new_rng_state(q, gen=None):
+    """CUDA int64 [seed, offset] drawn from `gen` (default: the device's CUDA
+    generator), without a host synchronisation."""
+    if gen is not None and not isinstance(gen, torch.Generator):
+        raise RuntimeError("gen must be a torch.Generator")
+    g = gen if gen is not None else torch.cuda.default_generators[q.device.index or 0]
+    return torch.randint(-(2**63), 2**63 - 1, (2,), device=q.device, dtype=torch.int64, generator=g)
+
+
+def _check_return_softmax(return_softmax, p):
+    if return_softmax and p == 0:
+        raise RuntimeError("return_softmax is only supported when p_dropout > 0.0")
+    if return_softmax:
+        raise NotImplementedError("diagnostic probabilities (return_softmax) are not part of this build")
 
 
 def _validate(q, k, v, out, alibi, softcap, *, packed=False):
@@ -78,9 +101,8 @@ def fwd(q, k, v, out=None, alibi_slopes=None, p_dropout=0.0, softmax_scale=None,
     """Return [output, LSE, probabilities, RNG state] (interface.py:732-852)."""
     if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
         _cpu_dispatch("fwd")
-    p = _check_dropout(p_dropout)
-    if return_softmax and p == 0:
-        raise RuntimeError("return_softmax is only supported when p_dropout > 0.0")
+    p = _check_dropout(p_dropout, softcap)
+    _check_return_softmax(return_softmax, p)
     _validate(q, k, v, out, alibi_slopes, softcap)
     if softmax_scale is None:
         softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
@@ -90,10 +112,15 @@ def fwd(q, k, v, out=None, alibi_slopes=None, p_dropout=0.0, softmax_scale=None,
         alibi_slopes = alibi_slopes.contiguous()
     if out is None:
         out = torch.empty_like(q)
-    lse = ops.fwd_lse(q, k, v, alibi_slopes, float(softmax_scale), bool(is_causal),
-                      int(window_size_left), int(window_size_right), float(softcap), out)
+    args = (q, k, v, alibi_slopes, float(softmax_scale), bool(is_causal), int(window_size_left),
+            int(window_size_right), float(softcap))
+    if p > 0:
+        state = _new_rng_state(q, gen)
+        lse = ops.fwd_lse(*args, p, state, 0, out)
+    else:
+        state = torch.empty(2, device=q.device, dtype=torch.int64)
+        lse = ops.fwd_lse(*args, out)
     probabilities = torch.empty(0, device=q.device, dtype=q.dtype)
-    state = torch.empty(2, device=q.device, dtype=torch.int64)
     return [out, lse, probabilities, state]
 
 
@@ -120,7 +147,7 @@ def bwd(dout, q, k, v, out, softmax_lse, dq=None, dk=None, dv=None, alibi_slopes
     deterministic and default paths are deterministic here (fixed-order GQA sums)."""
     if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
         _cpu_dispatch("bwd")
-    p = _check_dropout(p_dropout)
+    p = _check_dropout(p_dropout, softcap)
     _validate(q, k, v, None, alibi_slopes, softcap)
     for name, t in (("dout", dout), ("out", out)):
         if not isinstance(t, torch.Tensor) or t.shape != q.shape or t.device != q.device or t.dtype != q.dtype:
@@ -132,9 +159,12 @@ def bwd(dout, q, k, v, out, softmax_lse, dq=None, dk=None, dv=None, alibi_slopes
         softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.contiguous()
+    if p > 0 and rng_state is None:
+        rng_state = _new_rng_state(q, gen)  # as the reference: a fresh reservation
     delta = ops.bwd_preprocess(dout, out, p)
     args = (q, k, v, dout, softmax_lse, delta, alibi_slopes, float(softmax_scale), bool(is_causal),
-            int(window_size_left), int(window_size_right), float(softcap), p, None)
+            int(window_size_left), int(window_size_right), float(softcap), p,
+            rng_state if p > 0 else None)
     if deterministic:
         grad_q = ops.bwd_dq(*args)
         grad_k, grad_v = ops.bwd_dkv(*args)
@@ -165,9 +195,8 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, le
         _cpu_dispatch("varlen_fwd")
     if block_table is not None:
         raise NotImplementedError("paged K/V (block_table) is not supported by this build")
-    p = _check_dropout(p_dropout)
-    if return_softmax and p == 0:
-        raise RuntimeError("return_softmax is only supported when p_dropout > 0.0")
+    p = _check_dropout(p_dropout, softcap)
+    _check_return_softmax(return_softmax, p)
     _validate(q, k, v, out, alibi_slopes, softcap, packed=True)
     _check_varlen_meta(q, cu_seqlens_q, cu_seqlens_k)
     if not 0 <= int(max_seqlen_q) <= 2**31 - 128 or not 0 <= int(max_seqlen_k) <= 2**31 - 128:
@@ -176,15 +205,15 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, le
         softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.contiguous()
+    state = _new_rng_state(q, gen) if p > 0 else torch.empty(2, device=q.device, dtype=torch.int64)
     output, lse, probabilities = ops.varlen_fwd_explicit(
         q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi_slopes,
         float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),
-        float(softcap), p, None, int(max_seqlen_q), int(max_seqlen_k), bool(return_softmax),
-        bool(zero_tensors))
+        float(softcap), p, state if p > 0 else None, int(max_seqlen_q), int(max_seqlen_k),
+        bool(return_softmax), bool(zero_tensors))
     if out is not None:
         out.copy_(output)
         output = out
-    state = torch.empty(2, device=q.device, dtype=torch.int64)
     return [output, lse, probabilities, state]
 
 
@@ -195,7 +224,7 @@ def varlen_bwd(dout, q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, dq=N
     """Packed backward returning [dQ, dK, dV, softmax_d] (interface.py:1244-1471)."""
     if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
         _cpu_dispatch("varlen_bwd")
-    p = _check_dropout(p_dropout)
+    p = _check_dropout(p_dropout, softcap)
     if any(not isinstance(x, torch.Tensor) or x.ndim != 3 for x in (q, k, v)):
         raise RuntimeError("q, k, v must have shape [total_tokens, heads, head_size]")
     _validate(q, k, v, None, alibi_slopes, softcap, packed=True)
@@ -212,10 +241,13 @@ def varlen_bwd(dout, q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, dq=N
         softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.contiguous()
+    if p > 0 and rng_state is None:
+        rng_state = _new_rng_state(q, gen)
     grad_q, grad_k, grad_v, softmax_d = ops.varlen_bwd_explicit(
         q, k, v, dout, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, alibi_slopes,
         float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),
-        float(softcap), p, None, int(max_seqlen_q), int(max_seqlen_k), bool(zero_tensors))
+        float(softcap), p, rng_state if p > 0 else None, int(max_seqlen_q), int(max_seqlen_k),
+        bool(zero_tensors))
     return [*_finish_gradients((grad_q, grad_k, grad_v), (dq, dk, dv), (q, k, v)), softmax_d]
 
 

@@ -46,6 +46,34 @@ class KcrTensor(ctypes.Structure):
     ]
 
 
+class KcrDropout(ctypes.Structure):
+    """`kcr_dropout`: dropout probability and the Philox (seed, offset), or a
+    device int64 [2] RNG-state tensor holding them."""
+
+    _fields_ = [
+        ("p", ctypes.c_double),
+        ("seed", ctypes.c_uint64),
+        ("offset", ctypes.c_uint64),
+        ("rng_state", ctypes.POINTER(KcrTensor)),
+    ]
+
+
+def dropout_arg(p, seed=0, offset=0, state=None):
+    """A `kcr_dropout` reference (kept alive by the returned tuple's first item),
+    or None when p is 0."""
+    if not float(p) > 0.0:
+        return None, None
+    d = KcrDropout()
+    d.p = float(p)
+    d.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    d.offset = int(offset) & 0xFFFFFFFFFFFFFFFF
+    keep = None
+    if state is not None:
+        keep = describe(state)
+        d.rng_state = ctypes.pointer(keep)
+    return (d, keep), ctypes.byref(d)
+
+
 _ERRORS = {1: ValueError, 2: TypeError, 3: RuntimeError}
 
 
