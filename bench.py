@@ -98,7 +98,7 @@ def _attn_inputs(seed, b=4, hq=32, hkv=8, s=4096, d=128):
     return q, k, v
 
 
-def _wl_fa_fwd(causal):
+def _wl_fa_fwd(causal, p_dropout=0.0):
     def make():
         import flash_attn2_rs
 
@@ -106,20 +106,21 @@ def _wl_fa_fwd(causal):
         q, k, v = _attn_inputs(3, b, hq, hkv, s, d)
         out = torch.empty_like(q)
         ops = flash_attn2_rs.ops
+        drop = (p_dropout, 1234, 0) if p_dropout > 0 else ()
 
         def run():
-            ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, out)
+            ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, *drop, out)
 
         flops = 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
         return dict(run=run, work=flops, bound="mfma", kernel="flash_fwd",
                     config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
-                            "dtype": "bf16"},
+                            "dtype": "bf16", **({"p_dropout": p_dropout} if p_dropout else {})},
                     cpu=lambda: cpu_attention(q, k, v, causal))
 
     return make
 
 
-def _wl_fa_bwd(causal):
+def _wl_fa_bwd(causal, p_dropout=0.0):
     def make():
         import flash_attn2_rs
 
@@ -129,17 +130,19 @@ def _wl_fa_bwd(causal):
         dout = torch.randn(b, s, hq, d, generator=g).bfloat16().cuda()
         out = torch.empty_like(q)
         ops = flash_attn2_rs.ops
-        lse = ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, out)
-        args = (None, None, causal, -1, -1, 0.0, 0.0, None)
+        state = torch.tensor([1234, 0], dtype=torch.int64, device="cuda") if p_dropout > 0 else None
+        drop = (p_dropout, state, 0) if p_dropout > 0 else ()
+        lse = ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, *drop, out)
+        args = (None, None, causal, -1, -1, 0.0, p_dropout, state)
 
         def run():
-            delta = ops.bwd_preprocess(dout, out, 0.0)
+            delta = ops.bwd_preprocess(dout, out, p_dropout)
             ops.bwd_all(q, k, v, dout, lse, delta, *args)
 
         flops = 2.5 * 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
         return dict(run=run, work=flops, bound="mfma", kernel="flash_bwd_dkv",
                     config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
-                            "dtype": "bf16"},
+                            "dtype": "bf16", **({"p_dropout": p_dropout} if p_dropout else {})},
                     cpu=None)
 
     return make
@@ -210,6 +213,8 @@ WORKLOADS = {
     "fa_fwd": _wl_fa_fwd(False),
     "fa_bwd_causal": _wl_fa_bwd(True),
     "fa_bwd": _wl_fa_bwd(False),
+    "fa_fwd_causal_dropout": _wl_fa_fwd(True, 0.1),
+    "fa_bwd_causal_dropout": _wl_fa_bwd(True, 0.1),
     "fa_varlen_fwd": _wl_fa_varlen("fwd"),
     "fa_varlen_bwd": _wl_fa_varlen("bwd"),
     "rms_norm": wl_rmsnorm,
