@@ -45,6 +45,23 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     }
 }
 
+// Maximum of the 32 scores one lane holds (two 16-register halves) as a chain of
+// 16 v_maximum3_f32. IEEE maximum propagates NaN, which the row's output would
+// carry anyway; fmaxf would first quieten every operand (one extra v_max each).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+__device__ __forceinline__ float lane_max32(const f32x16& a, const f32x16& b) {
+    float m0 = max3f(a[0], a[1], a[2]);
+    float m1 = max3f(b[0], b[1], b[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) {
+        m0 = max3f(m0, a[r], a[r + 1]);
+        m1 = max3f(m1, b[r], b[r + 1]);
+    }
+    return max3f(m0, m1, __builtin_elementwise_maximum(a[15], b[15]));
+}
+
 // Buffer resource over `bytes` bytes at `base`: loads at offsets >= bytes return 0
 // (hardware range check), which zero-fills the tile rows past the sequence end.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

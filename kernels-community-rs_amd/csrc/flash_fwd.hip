@@ -342,12 +342,7 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
                     }
                 }
             }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[qt][sub][r], s[qt][sub][r + 1]));
-            }
+            float mx = lane_max32(s[qt][0], s[qt][1]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float m2 = mx * c;
             // Rescale O and l only when some row's max grew by more than the slack:
@@ -612,12 +607,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
                 }
             }
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[sub][r], s[sub][r + 1]));
-        }
+        float mx = lane_max32(s[0], s[1]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m2 = mx * c;
         // Lazy rescale: the running max moves only when some row's max grows by
