@@ -312,6 +312,64 @@ __device__ __forceinline__ void copy_rows(const uint16_t* base, int64_t row_stri
     }
 }
 
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E - 1.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Direct HBM -> LDS copy issued from inline assembly: 16 bytes per lane from the
+// buffer `rsrc` (descriptor words) at `voffset` into LDS at `lds_base` + 16 * lane.
+// The compiler does not see these copies, so it inserts no wait for them before
+// later LDS reads; the caller orders them with explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma_lds16(const u32x4& rsrc, uint32_t lds_base, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_base)))
+                 : "memory", "m0");
+}
+
+// Raw buffer descriptor over `bytes` bytes at `base` (stride 0, same flags as make_rsrc).
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const auto rfl = [](uint32_t x) {
+        return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+    };
+    return u32x4{rfl(static_cast<uint32_t>(a)), rfl(static_cast<uint32_t>(a >> 32) & 0xFFFFu), rfl(bytes),
+                 0x00020000u};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+
+// copy_rows through dma_lds16: the same tile, rows and zero fill.
+template <int D, int NW, int ROWS>
+__device__ __forceinline__ void copy_rows_dma(const uint16_t* base, int64_t row_stride, int rows_valid,
+                                              uint16_t* tile, int wave, int lane) {
+    constexpr int CH = D / 8;
+    constexpr int RPB = 64 / CH;
+    constexpr int NBLK = ROWS / RPB;
+    static_assert(NBLK % NW == 0, "tile blocks must divide among the waves");
+    constexpr int IPW = NBLK / NW;
+    const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 2u;
+    const uint32_t bytes =
+        rows_valid > 0 ? static_cast<uint32_t>((min(rows_valid, ROWS) - 1) * row_stride + D) * 2u : 0u;
+    const u32x4 r = rsrc_words(base, bytes);
+    const uint32_t tile_lds = lds_addr(tile);
+    const int rr = lane / CH;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        const int blk = wave * IPW + i;
+        const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * RPB + rr);
+        dma_lds16(r, tile_lds + blk * 1024u, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u);
+    }
+}
+
 // Per-lane parts of the swizzled tile addresses. The swizzle of a row depends
 // only on row bits that the compile-time parts of the reads (32-row halves,
 // 16-row groups) leave unchanged, so each read is the lane base plus a

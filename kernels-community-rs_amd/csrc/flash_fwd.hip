@@ -681,6 +681,317 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     }
 }
 
+// ---------------------------------------------------------------------------
+// Ping-pong forward (plain scaled dot product, head size 128, dense grid with
+// no mask or dropout): 8 waves, 256 query rows per block, one block per CU.
+// Waves 0-3 and 4-7 form two groups on the same four SIMDs (wave w runs on
+// SIMD w % 4). Every slot of the loop ends at a block barrier; in each slot one
+// group runs its MFMA phase (O^T += V^T P^T of the previous tile, then
+// S^T = K Q^T of the current one) while the other runs its softmax phase
+// (row max, exp2, row sum, P^T packing). One group trails the other by a slot,
+// so on every SIMD the matrix core and the VALU serve different waves at the
+// same time instead of both waves reaching the same phase together.
+//
+// What bounds it: an MFMA phase reads 32 KB of LDS operands per wave, and with
+// one reading wave per SIMD the LDS delivers about half the bandwidth it gives
+// two (about 97 vs 193 B/clk/CU for 16-byte reads, measured), so the phase
+// runs about 1.9k cycles for 1k cycles of MFMA. It beats the 128-row tiled
+// kernel on unmasked grids (+5 %); on causal, windowed and dropout grids the
+// tiled kernel wins (diagonal waste of 256-row blocks, longer softmax phases).
+//
+// K/V tiles of 64 keys go HBM -> LDS by direct buffer loads into a ring of 4
+// stages. Tile j is read in slots 2j .. 2j + 3 (K by the MFMA phases of tile j,
+// V by those of tile j + 1); its copy is issued in slot 2j - 4 and must have
+// landed by the end of slot 2j - 1, so three slots hide its latency. The copies
+// are issued from inline assembly: the compiler would otherwise wait for every
+// copy in flight before the next LDS read.
+// ---------------------------------------------------------------------------
+constexpr int kPPStages = 4;
+
+
+// Slot boundary: this wave's LDS reads are complete, then the block barrier.
+// The asm memory clobber keeps memory operations on their side; the scheduling
+// barriers keep every other instruction on its side too.
+__device__ __forceinline__ void slot_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt at their maximum (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p) {
+    constexpr int NW = 8;
+    constexpr int BN = kBN;
+    constexpr int BM = 32 * NW;
+    constexpr int KS = D / 16;
+    constexpr int DB = D / 32;
+    constexpr int TILE = BN * D;
+    constexpr int STAGE = 2 * TILE;  // K tile, then V tile
+    // Direct loads each wave issues per tile (K and V): its vmcnt share.
+    constexpr int LPT = 2 * (BN * D / 512) / NW;
+    static_assert(LPT > 0 && LPT < 16, "loads per tile");
+
+    __shared__ __attribute__((aligned(1024))) uint16_t kv_lds[kPPStages * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    // Waves 4-7 lead (measured slightly faster than waves 0-3 leading).
+    const int grp = (wave >> 2) ^ 1;
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;
+    TileLane<D> tl(lane);
+
+    // Sequence-major order: the blocks of one (batch, KV head) run together and
+    // share its K/V tiles in L2.
+    const int per_seq = p.q_blocks * p.heads;
+    const int b = blockIdx.x / per_seq;
+    const int rem = blockIdx.x - b * per_seq;
+    const int qo = rem / p.heads;
+    const int idx = rem - qo * p.heads;
+    const int head = (idx % p.kv_heads) * p.gqa + idx / p.kv_heads;
+    const int kvh = head / p.gqa;
+    const int qb = p.q_blocks - 1 - qo;
+    const int sq = p.seqlen_q, sk = p.seqlen_k;
+    const int row0 = qb * BM;
+    if (row0 >= sq) return;
+
+    const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + b * p.k_b + kvh * p.k_h;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + b * p.v_b + kvh * p.v_h;
+    uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.o_b + head * p.o_h;
+    float* lse_base = p.lse + b * p.lse_b + head * p.lse_h;
+
+    const int n = (sk + BN - 1) / BN;
+
+    const int row = row0 + 32 * wave + l32;
+
+    u32x4 qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = row < sq ? *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + 16 * ks + 8 * hh)
+                          : u32x4{0, 0, 0, 0};
+    }
+    const float c = p.scale_log2;
+
+    f32x16 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = f32x16{};
+    f32x16 sc[2] = {f32x16{}, f32x16{}};
+    u32x4 pk[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) pk[tt] = u32x4{0, 0, 0, 0};
+    float m = -INFINITY, l = 0.0f;
+
+    auto copy_tile = [&](int t) __attribute__((always_inline)) {
+        const int kb = t * BN;
+        uint16_t* st = kv_lds + (t % kPPStages) * STAGE;
+        copy_rows_dma<D, NW, BN>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, st, wave, lane);
+        copy_rows_dma<D, NW, BN>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, st + TILE, wave,
+                                 lane);
+    };
+
+    // MFMA phase of step t: O^T += V^T P^T for tile t - 1, then S^T = K Q^T for
+    // tile t. The operand reads run kLook MFMAs ahead of their use (register
+    // ring), interleaved one MFMA at a time.
+    auto mphase_impl = [&](auto pv_tag, auto qk_tag, int t) __attribute__((always_inline)) {
+        constexpr bool PV = decltype(pv_tag)::value;
+        constexpr bool QK = decltype(qk_tag)::value;
+        constexpr int NPV = PV ? 4 * DB : 0;
+        constexpr int NQK = QK ? 2 * KS : 0;
+        constexpr int N = NPV + NQK;
+        constexpr int LOOK = 4;
+        const uint16_t* vl = kv_lds + ((t + kPPStages - 1) % kPPStages) * STAGE + TILE;
+        const uint16_t* kl = kv_lds + (t % kPPStages) * STAGE;
+        // PV step i: tt = i / DB, db = i % DB (consecutive MFMAs use different
+        // accumulators); QK step j: half j % 2, k-step j / 2.
+        auto load = [&](auto ic) __attribute__((always_inline)) -> u32x4 {
+            constexpr int i = decltype(ic)::value;
+            if constexpr (i < NPV) {
+                return tl.tr(vl, i % DB, i / DB);
+            } else {
+                return tl.rm(kl, (i - NPV) & 1, (i - NPV) >> 1);
+            }
+        };
+        // The MFMA-phase wave takes issue priority over the softmax-phase wave
+        // of its SIMD (otherwise the older wave of the pair wins arbitration
+        // whichever phase it is in).
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        tl.refresh();
+        if constexpr (QK) {
+            sc[0] = f32x16{};
+            sc[1] = f32x16{};
+        }
+        u32x4 ring[LOOK];
+        constexpr int NPRO = LOOK < N ? LOOK : N;
+        static_for<0, NPRO>([&](auto ic) __attribute__((always_inline)) { ring[decltype(ic)::value] = load(ic); });
+        // Reads of the first NPRO operands, then (reads of operand i + LOOK, MFMA i).
+        constexpr int PRO_READS = 2 * (NPRO < NPV ? NPRO : NPV) + (NPRO > NPV ? NPRO - NPV : 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, PRO_READS, 0);
+        static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            const u32x4 a = ring[i % LOOK];
+            if constexpr (i + LOOK < N) {
+                ring[i % LOOK] = load(std::integral_constant<int, i + LOOK>{});
+                __builtin_amdgcn_sched_group_barrier(0x100, (i + LOOK < NPV) ? 2 : 1, 0);
+            }
+            if constexpr (i < NPV) {
+                o[i % DB] = mfma32<T>(a, pk[i / DB], o[i % DB]);
+            } else {
+                constexpr int j = i - NPV;
+                sc[j & 1] = mfma32<T>(a, qf[j >> 1], sc[j & 1]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // Softmax phase of tile t: P^T packed into the B operand of the next MFMA phase.
+    auto vphase = [&](int t) __attribute__((always_inline)) {
+        // Only the last tile can cross the end of the keys.
+        const int kb = t * BN;
+        if (kb + BN > sk) {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    sc[sub][r] = col >= sk ? -INFINITY : sc[sub][r];
+                }
+            }
+        }
+        float mx = lane_max32(sc[0], sc[1]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m2 = mx * c;
+        if (__any(m2 > m + kRescaleSlack)) {
+            const float m_new = fmaxf(m, m2);
+            const float alpha = (m_new == -INFINITY) ? 1.0f : fast_exp2(m - m_new);
+            m = m_new;
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[db] *= alpha;
+        }
+        const float neg_m = (m == -INFINITY) ? 0.0f : -m;
+        float rowsum = 0.0f;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pv = fast_exp2(__builtin_fmaf(sc[sub][r], c, neg_m));
+                sc[sub][r] = pv;
+                rowsum += pv;
+            }
+        }
+        l += rowsum;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                pk[tt][w] = pack2<T>(sc[tt >> 1][8 * (tt & 1) + 2 * w], sc[tt >> 1][8 * (tt & 1) + 2 * w + 1]);
+            }
+        }
+    };
+
+    // Slot s: even slots issue the copy of tile s / 2 + 2; odd slot 2k + 1 ends
+    // with tile k + 1 resident (tile k + 2 may still be in flight).
+    auto slot_begin = [&](int s) __attribute__((always_inline)) {
+        if ((s & 1) == 0 && s / 2 + 2 < n) copy_tile(s / 2 + 2);
+    };
+    auto slot_end = [&](int s) __attribute__((always_inline)) {
+        if (s & 1) {
+            if (s / 2 + 2 < n) {
+                wait_vmem_le<LPT>();
+            } else {
+                wait_vmem_le<0>();
+            }
+        }
+        slot_barrier();
+    };
+
+    if (n > 0) copy_tile(0);
+    if (n > 1) {
+        copy_tile(1);
+        wait_vmem_le<LPT>();
+    } else {
+        wait_vmem_le<0>();
+    }
+    slot_barrier();
+
+    // The first and last MFMA phases (QK only, PV only) are peeled so the
+    // steady-state loop body is one straight-line sequence per group.
+    const std::true_type yes{};
+    const std::false_type no{};
+    if (n > 0) {
+        if (grp == 0) {
+            slot_begin(0);
+            mphase_impl(no, yes, 0);
+            slot_end(0);
+            slot_begin(1);
+            vphase(0);
+            slot_end(1);
+            for (int t = 1; t < n; ++t) {
+                slot_begin(2 * t);
+                mphase_impl(yes, yes, t);
+                slot_end(2 * t);
+                slot_begin(2 * t + 1);
+                vphase(t);
+                slot_end(2 * t + 1);
+            }
+            slot_begin(2 * n);
+            mphase_impl(yes, no, n);
+            slot_end(2 * n);
+            slot_begin(2 * n + 1);
+            slot_end(2 * n + 1);
+        } else {
+            slot_begin(0);
+            slot_end(0);
+            slot_begin(1);
+            mphase_impl(no, yes, 0);
+            slot_end(1);
+            for (int t = 1; t < n; ++t) {
+                slot_begin(2 * t);
+                vphase(t - 1);
+                slot_end(2 * t);
+                slot_begin(2 * t + 1);
+                mphase_impl(yes, yes, t);
+                slot_end(2 * t + 1);
+            }
+            slot_begin(2 * n);
+            vphase(n - 1);
+            slot_end(2 * n);
+            slot_begin(2 * n + 1);
+            mphase_impl(yes, no, n);
+            slot_end(2 * n + 1);
+        }
+    }
+
+    const float lt = l + __shfl_xor(l, 32, 64);
+    if (row < sq) {
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        uint16_t* orow = obase + row * p.o_s;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * hh;
+                uint2 w;
+                w.x = pack2<T>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+                w.y = pack2<T>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+                *reinterpret_cast<uint2*>(orow + d) = w;
+            }
+        }
+        if (hh == 0) lse_base[row] = lt > 0.0f ? (m + fast_log2(lt)) * kLn2 : INFINITY;
+    }
+}
+
 // Empty-key rows: O = 0, LSE = +inf (host/forward/mod.rs:548-572). Also clears
 // the output when zero_tensors is requested. Uses kernels rather than
 // hipMemsetAsync so the calls stay safe inside captured graphs.
@@ -768,9 +1079,30 @@ void launch_tiled(FwdParams& prm, hipStream_t s) {
 }
 
 template <typename T, int D, bool VARLEN>
+void launch_pp(FwdParams& prm, hipStream_t s) {
+    constexpr int BM = 256;
+    prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
+    const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads;
+    if (blocks == 0) return;
+    if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
+    prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
+    prm.seq_major = 1;
+    flash_fwd_pp_kernel<T, D><<<static_cast<unsigned>(blocks), 512, 0, s>>>(prm);
+    check_launch("launch flash_fwd");
+}
+
+template <typename T, int D, bool VARLEN>
 void launch_d(FwdParams& prm, bool general, hipStream_t s) {
     if constexpr (D == 64 || D == 128) {
         if (!general) {
+            // Dense unmasked D = 128 without dropout: the ping-pong kernel
+            // (measured faster there; the 128-row tiled kernel wins on causal,
+            // windowed, dropout, packed and D = 64 grids).
+            if constexpr (D == 128 && !VARLEN) {
+                if (prm.window_left < 0 && prm.window_right < 0 && prm.drop_threshold == 255) {
+                    return launch_pp<T, D, VARLEN>(prm, s);
+                }
+            }
             return launch_tiled<T, D, VARLEN>(prm, s);
         }
     }

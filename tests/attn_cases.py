@@ -36,6 +36,7 @@ PARITY_CASES = [
     case("window-sq384-sk256-wl64", 1, 4, 4, 384, 256, causal=True, window_left=64),
     case("odd-causal-s333", 2, 4, 4, 333, 333, causal=True),
     case("odd-full-s200", 2, 4, 4, 200, 200),
+    case("odd-full-gqa-sq600-sk700", 1, 8, 2, 600, 700),
     case("odd-gqa-causal-s130", 2, 8, 2, 130, 130, causal=True),
     case("odd-sq100-sk250", 1, 4, 4, 100, 250, causal=True),
     case("odd-window-softcap-s300", 1, 4, 4, 300, 300, causal=True, window_left=100, softcap=30.0),
