@@ -267,50 +267,9 @@ __device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(uint2, v);
 }
 
-// Direct HBM -> LDS copy: 16 bytes per lane from `r` at voffset + soffset into
-// LDS at lds_base + 16 * lane (a wave moves 1 KB, lane order).
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, const void* lds_base,
-                                           uint32_t voffset, uint32_t soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset, soffset, 0, 0);
-}
-
-// Same with 4 bytes per lane (a wave moves 256 bytes).
-__device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, const void* lds_base,
-                                          uint32_t voffset, uint32_t soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)(lds_base), 4, voffset, soffset, 0, 0);
-}
-
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maximum);
 // the direct LDS copies are tracked by vmcnt.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
-// elements) into a swizzled tile; rows at or past `rows_valid` read as zero.
-// The NW waves move 1 KB blocks of 8 (D = 64) or 4 (D = 128) rows.
-template <int D, int NW, int ROWS>
-__device__ __forceinline__ void copy_rows(const uint16_t* base, int64_t row_stride, int rows_valid,
-                                          uint16_t* tile, int wave, int lane) {
-    constexpr int CH = D / 8;
-    constexpr int RPB = 64 / CH;
-    constexpr int NBLK = ROWS / RPB;
-    static_assert(NBLK % NW == 0, "tile blocks must divide among the waves");
-    constexpr int IPW = NBLK / NW;
-    const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 2u;
-    const uint32_t bytes =
-        rows_valid > 0 ? static_cast<uint32_t>((min(rows_valid, ROWS) - 1) * row_stride + D) * 2u : 0u;
-    const auto r = make_rsrc(base, bytes);
-    const int rr = lane / CH;
-#pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-        const int blk = wave * IPW + i;
-        const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * RPB + rr);
-        // Whole offset in voffset: the range check that zero-fills rows past the
-        // end covers voffset only.
-        load_lds16(r, tile + blk * 512, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u, 0);
-    }
-}
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E - 1.
 template <int B, int E, typename F>
@@ -332,6 +291,14 @@ __device__ __forceinline__ void dma_lds16(const u32x4& rsrc, uint32_t lds_base, 
                  : "memory", "m0");
 }
 
+// Same with 4 bytes per lane (LDS at `lds_base` + 4 * lane).
+__device__ __forceinline__ void dma_lds4(const u32x4& rsrc, uint32_t lds_base, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_base)))
+                 : "memory", "m0");
+}
+
 // Raw buffer descriptor over `bytes` bytes at `base` (stride 0, same flags as make_rsrc).
 __device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(base);
@@ -347,7 +314,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
         reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
 }
 
-// copy_rows through dma_lds16: the same tile, rows and zero fill.
+// Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
+// elements) into a swizzled tile by direct HBM -> LDS loads; rows at or past
+// `rows_valid` read as zero (buffer range check). The NW waves move 1 KB blocks
+// of 8 (D = 64) or 4 (D = 128) rows.
 template <int D, int NW, int ROWS>
 __device__ __forceinline__ void copy_rows_dma(const uint16_t* base, int64_t row_stride, int rows_valid,
                                               uint16_t* tile, int wave, int lane) {

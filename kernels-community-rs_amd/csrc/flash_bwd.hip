@@ -684,8 +684,8 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     const int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
 
     auto copy_tile = [&](int kb, int stage) {
-        copy_rows<D, NW, 64>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE, wave, lane);
-        copy_rows<D, NW, 64>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, 64>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, 64>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE, wave, lane);
     };
     if (ntiles > 0) {
         copy_tile(kv_begin, 0);
@@ -839,7 +839,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
         }
     }
     if constexpr (V_LDS) {
-        copy_rows<D, NW, BK>(vbase + static_cast<int64_t>(key0) * p.v_s, p.v_s, sk - key0, v_lds, wave, lane);
+        copy_rows_dma<D, NW, BK>(vbase + static_cast<int64_t>(key0) * p.v_s, p.v_s, sk - key0, v_lds, wave, lane);
     }
     f32x16 dk[DB], dv[DB];
 #pragma unroll
@@ -871,17 +871,17 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
         const int head = kvh * p.gqa + j;
         const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head * p.q_h;
         const uint16_t* dobase = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) + head * p.do_h;
-        copy_rows<D, NW, BQ>(qbase + static_cast<int64_t>(qb) * p.q_s, p.q_s, sq - qb, q_lds + stage * TILE, wave, lane);
-        copy_rows<D, NW, BQ>(dobase + static_cast<int64_t>(qb) * p.do_s, p.do_s, sq - qb, do_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, BQ>(qbase + static_cast<int64_t>(qb) * p.q_s, p.q_s, sq - qb, q_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, BQ>(dobase + static_cast<int64_t>(qb) * p.do_s, p.do_s, sq - qb, do_lds + stage * TILE, wave, lane);
         // Rows past the sequence read LSE 0 and delta 0; their Q and dO rows are
         // zero, so they add nothing to dK and dV.
         const uint32_t rows = static_cast<uint32_t>(max(0, min(sq - qb, BQ)));
         if (wave == 0) {
             const float* lse_row = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + sb.lse_row0 + qb;
-            load_lds4(make_rsrc(lse_row, rows * 4u), lse_lds + stage * 64, lane * 4u, 0);
+            dma_lds4(rsrc_words(lse_row, rows * 4u), lds_addr(lse_lds + stage * 64), lane * 4u);
         } else if (wave == 1) {
             const float* dl_row = p.delta + (VARLEN ? 0 : b * p.delta_b) + head * p.delta_h + sb.delta_row0 + qb;
-            load_lds4(make_rsrc(dl_row, rows * 4u), dl_lds + stage * 64, lane * 4u, 0);
+            dma_lds4(rsrc_words(dl_row, rows * 4u), lds_addr(dl_lds + stage * 64), lane * 4u);
         }
     };
     if (ntiles > 0) copy_tile(0, 0);

@@ -566,9 +566,9 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     float m = -INFINITY, l = 0.0f;
 
     auto copy_tile = [&](int kb, int stage) {
-        copy_rows<D, NW, BN>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE,
+        copy_rows_dma<D, NW, BN>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE,
                              wave, lane);
-        copy_rows<D, NW, BN>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE,
+        copy_rows_dma<D, NW, BN>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE,
                              wave, lane);
     };
 
