@@ -46,7 +46,8 @@ __device__ __forceinline__ int vt_swizzle(int row) {
     const int x = (row >> 4) & 7;
     return (x & 1) | ((x & 6) << 1);
 }
-constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag behind
+constexpr float kRescaleSlack = 8.0f;
+constexpr int kLookTiled = 4;  // operand reads in flight ahead of their MFMA (tiled kernel)  // log2 units the running max may lag behind
 
 // GENERAL covers softcap, ALiBi and head sizes below the compiled bucket (zeroed
 // lanes of the padded head dimension); the fast path is the plain scaled dot
@@ -585,12 +586,27 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         const uint16_t* vl = v_lds + (t & 1) * TILE;
         if (t + 1 < ntiles) copy_tile(kb + BN, (t + 1) & 1);
 
-        // S^T = K Q^T for the 64 keys of the tile (two 32-key halves).
+        // S^T = K Q^T for the 64 keys of the tile (two 32-key halves); the K
+        // reads run kLookTiled MFMAs ahead of their use.
         f32x16 s[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            s[0] = mfma32<T>(tl.rm(kl, 0, ks), qf[ks], s[0]);
-            s[1] = mfma32<T>(tl.rm(kl, 1, ks), qf[ks], s[1]);
+        {
+            constexpr int N = 2 * KS;
+            u32x4 ring[kLookTiled];
+            static_for<0, kLookTiled>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                ring[i] = tl.rm(kl, i & 1, i >> 1);
+            });
+            __builtin_amdgcn_sched_group_barrier(0x100, kLookTiled, 0);
+            static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                const u32x4 a = ring[i % kLookTiled];
+                if constexpr (i + kLookTiled < N) {
+                    ring[i % kLookTiled] = tl.rm(kl, (i + kLookTiled) & 1, (i + kLookTiled) >> 1);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                s[i & 1] = mfma32<T>(a, qf[i >> 1], s[i & 1]);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            });
         }
 
         const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
@@ -652,11 +668,25 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
                 pk[tt][w] = pack2<T>(s[tt >> 1][8 * (tt & 1) + 2 * w], s[tt >> 1][8 * (tt & 1) + 2 * w + 1]);
             }
         }
-        // O^T += V^T P^T
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) o[db] = mfma32<T>(tl.tr(vl, db, tt), pk[tt], o[db]);
+        // O^T += V^T P^T (step i: db = i % DB, tt = i / DB), reads ahead as above.
+        {
+            constexpr int N = 4 * DB;
+            u32x4 ring[kLookTiled];
+            static_for<0, kLookTiled>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                ring[i] = tl.tr(vl, i % DB, i / DB);
+            });
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLookTiled, 0);
+            static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                const u32x4 a = ring[i % kLookTiled];
+                if constexpr (i + kLookTiled < N) {
+                    ring[i % kLookTiled] = tl.tr(vl, (i + kLookTiled) % DB, (i + kLookTiled) / DB);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+                o[i % DB] = mfma32<T>(a, pk[i / DB], o[i % DB]);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            });
         }
         wait_vmem();
         __syncthreads();
