@@ -161,6 +161,46 @@ int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_ten
                          int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
                          const kcr_tensor* out, const kcr_tensor* lse, void* stream);
 
+/* KV-cache append. replaces `cache_update_explicit(q, kcache, vcache, k, v, lengths,
+ * cos, sin, indices, table, interleaved, advance_q)` (flash-attn2-rs/src/host/cache/
+ * mod.rs:36-320, kernel src/device/cache.rs:26-330).
+ *   New rows k/v [B, Snew, Hk, D] go to cache position seqlens[b] + r of cache batch
+ *   cache_batch_idx[b] (or b), or of page block_table[b, position / page] (page =
+ *   kcache.shape[1], a multiple of 256). kcache/vcache [batches | pages, rows, Hk, D].
+ *   With rotary_cos/sin [positions, rotary_dim / 2] (q's dtype), K is rotated at its
+ *   position and q into q_out at seqlens[b] + (advance_q ? r : 0); interleaved pairs
+ *   columns (2i, 2i + 1), otherwise (i, i + rotary_dim / 2). q_out may be NULL
+ *   without rotary tables. */
+int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
+                           const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* seqlens,
+                           const kcr_tensor* rotary_cos, const kcr_tensor* rotary_sin,
+                           const kcr_tensor* cache_batch_idx, const kcr_tensor* block_table,
+                           int interleaved, int advance_q, const kcr_tensor* q_out, void* stream);
+
+/* Attention over a KV cache. replaces the cached mode of `varlen_fwd_explicit`
+ * (args 19-23: block_table, cache_batch_idx, new_keys, num_splits, grouped;
+ * flash-attn2-rs/src/host/varlen/mod.rs:36-670, device/varlen/mod.rs:60-170,
+ * device/varlen/paged.rs, device/varlen/merge.rs).
+ *   q [Tq, H, D] packed with cu_seqlens_q int32 [B+1]; sequence b attends to cache
+ *   rows [leftpad_k[b], seqused_k[b]) (seqused_k = cache lengths after the append)
+ *   of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
+ *   (int32 [B, max_blocks]; head size 64 or 128, no softcap/ALiBi). out like q;
+ *   lse float32 [H, Tq]. Windows are normalised against the cache capacity.
+ *   num_splits > 1 splits each query tile's keys over that many blocks; the fp32
+ *   partials go to `workspace` (kcr_flash_fwd_kvcache_workspace_bytes bytes,
+ *   16-byte aligned) and a merge kernel writes out/lse. Softcap / ALiBi / other
+ *   head sizes run unsplit. */
+int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int64_t heads, int64_t total_q,
+                                              int64_t head_dim);
+int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
+                          const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k,
+                          const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                          const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
+                          double scale, int causal, int64_t window_left, int64_t window_right,
+                          double softcap, int64_t max_seqlen_q, int64_t num_splits, void* workspace,
+                          int64_t workspace_bytes, const kcr_tensor* out, const kcr_tensor* lse,
+                          void* stream);
+
 /* Backward preprocess. replaces `bwd_preprocess(dout, out, p)`
  * (flash-attn2-rs/src/host/backward.rs:628-737):
  *   delta[b,h,s] = sum_d dout*out * (1-p), float32 [B,H,round128(Sq)], rows >= Sq are 0. */

@@ -115,7 +115,74 @@ struct FwdParams {
     float scale_log2;            // softmax scale * log2(e), no softcap
     float tanh_scale;            // softcap: tanh(raw * tanh_scale) * scale_eff
     float scale_eff_log2;        // softcap: softcap * sign(scale) * log2(e)
+    // KV-cache mode (varlen kernels; flash-attn2-rs/src/device/varlen/mod.rs:60-170
+    // with CACHED): the keys of sequence b are rows [leftpad_k[b], seqused_k[b])
+    // of cache batch cache_idx[b] (or b), or of the pages block_table[b, :].
+    int32_t cache_mode;
+    int32_t capacity;            // rows per cache batch (or table_cols * page_size)
+    int32_t cache_batches;       // cache batches (or pages)
+    const int32_t* cache_idx;
+    const int32_t* block_table;  // paged K/V: [batch, table_cols] page indices
+    int64_t table_stride;
+    int32_t table_cols;
+    int32_t page_size;           // rows per page, a multiple of the 64-row tile
+    int64_t k_page, v_page;      // element strides between pages
+    // Split-KV (tiled varlen kernel): n_splits > 1 writes per-split fp32 partials
+    // o_part [n_splits, H, Tq, D] (normalised) and lse_part [n_splits, H, Tq].
+    int32_t n_splits;
+    float* o_part;
+    float* lse_part;
 };
+
+// Packed-sequence bounds of sequence b (device/varlen/mod.rs:79-136): query rows
+// [qs, qs + sq) of the packed q, keys from row k_row0 of K batch k_batch (cache
+// mode) or of the packed K. Metadata is trusted as in the reference; only memory
+// bounds are guarded (ok = false: the block writes nothing).
+struct VarSeq {
+    int sq, sk, qs;
+    int64_t k_row0, k_batch;
+    bool ok;
+};
+
+__device__ __forceinline__ VarSeq varlen_seq(const FwdParams& p, int b) {
+    VarSeq r{};
+    const int qs = p.cu_q[b];
+    const int qe = p.cu_q[b + 1];
+    int ks = 0, ke = p.capacity;
+    int64_t kbatch = 0;
+    if (p.cache_mode) {
+        if (!p.block_table) {
+            kbatch = p.cache_idx ? p.cache_idx[b] : b;
+            if (kbatch < 0 || kbatch >= p.cache_batches) return r;
+        }
+    } else {
+        ks = p.cu_k[b];
+        ke = p.cu_k[b + 1];
+    }
+    const int len = p.seqused_k ? p.seqused_k[b] : ke - ks;
+    const int pad = p.leftpad_k ? p.leftpad_k[b] : 0;
+    if (qs < 0 || qe < qs || qe > p.total_q || ks < 0 || ke < ks || (!p.cache_mode && ke > p.total_k) ||
+        pad < 0 || len < pad || len > ke - ks || qe - qs > p.seqlen_q) {
+        return r;
+    }
+    r.sq = qe - qs;
+    r.sk = len - pad;
+    r.qs = qs;
+    r.k_row0 = static_cast<int64_t>(ks + pad);
+    r.k_batch = kbatch;
+    r.ok = true;
+    return r;
+}
+
+// Paged K/V: the page of the block table that holds key row kb of sequence b
+// (tiles never cross pages: pages are multiples of the tile). Returns -1 for
+// entries outside the table or the cache; such tiles read as zero.
+__device__ __forceinline__ int64_t page_of(const FwdParams& p, int b, int kb) {
+    const int col = kb / p.page_size;
+    if (col >= p.table_cols) return -1;
+    const int page = p.block_table[static_cast<int64_t>(b) * p.table_stride + col];
+    return (page >= 0 && page < p.cache_batches) ? page : -1;
+}
 
 // Host-side normalisation of the attention options shared by all entry points.
 struct Options {

@@ -104,23 +104,16 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     int64_t q_off = 0, k_off = 0;
     int sq = p.seqlen_q, sk = p.seqlen_k;
     int lse_row0 = 0;
+    int64_t k_batch = 0;
     if constexpr (VARLEN) {
-        const int qs = p.cu_q[b];
-        const int qe = p.cu_q[b + 1];
-        const int ks = p.cu_k[b];
-        const int ke = p.cu_k[b + 1];
-        const int len = p.seqused_k ? p.seqused_k[b] : ke - ks;
-        const int pad = p.leftpad_k ? p.leftpad_k[b] : 0;
-        // Metadata is trusted as in the reference; only memory bounds are guarded.
-        if (qs < 0 || qe < qs || qe > p.total_q || ks < 0 || ke < ks || ke > p.total_k || pad < 0 ||
-            len < pad || len > ke - ks || qe - qs > p.seqlen_q) {
-            return;
-        }
-        sq = qe - qs;
-        sk = len - pad;
-        q_off = static_cast<int64_t>(qs);
-        k_off = static_cast<int64_t>(ks + pad);
-        lse_row0 = qs;
+        const VarSeq vs = varlen_seq(p, b);
+        if (!vs.ok) return;
+        sq = vs.sq;
+        sk = vs.sk;
+        q_off = static_cast<int64_t>(vs.qs);
+        k_off = vs.k_row0;
+        k_batch = vs.k_batch;
+        lse_row0 = vs.qs;
         qb = (sq + BM - 1) / BM - 1 - qo;
         if (qb < 0) return;
     }
@@ -136,8 +129,8 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     uint16_t* obase;
     if constexpr (VARLEN) {
         qbase = static_cast<const uint16_t*>(p.q) + q_off * p.q_s + head * p.q_h;
-        kbase = static_cast<const uint16_t*>(p.k) + k_off * p.k_s + kvh * p.k_h;
-        vbase = static_cast<const uint16_t*>(p.v) + k_off * p.v_s + kvh * p.v_h;
+        kbase = static_cast<const uint16_t*>(p.k) + k_batch * p.k_b + k_off * p.k_s + kvh * p.k_h;
+        vbase = static_cast<const uint16_t*>(p.v) + k_batch * p.v_b + k_off * p.v_s + kvh * p.v_h;
         obase = static_cast<uint16_t*>(p.o) + q_off * p.o_s + head * p.o_h;
     } else {
         qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
@@ -197,11 +190,22 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     auto load_tile = [&](int kb) {
         // Valid bytes from the tile's first row: rows >= sk (and the padded head
         // dims of the last row) fall outside the range and read as zero.
-        const int rows = min(sk - kb, BN);
+        int rows = min(sk - kb, BN);
+        const uint16_t* kt = kbase + static_cast<int64_t>(kb) * p.k_s;
+        const uint16_t* vt = vbase + static_cast<int64_t>(kb) * p.v_s;
+        if constexpr (VARLEN) {
+            if (p.block_table) {
+                const int64_t page = page_of(p, b, kb);
+                const int64_t within = kb % p.page_size;
+                kt = kbase + page * p.k_page + within * p.k_s;
+                vt = vbase + page * p.v_page + within * p.v_s;
+                if (page < 0) rows = 0;
+            }
+        }
         const uint32_t kbytes = rows > 0 ? static_cast<uint32_t>((rows - 1) * p.k_s + p.head_dim) * 2u : 0u;
         const uint32_t vbytes = rows > 0 ? static_cast<uint32_t>((rows - 1) * p.v_s + p.head_dim) * 2u : 0u;
-        const auto kr = make_rsrc(kbase + static_cast<int64_t>(kb) * p.k_s, kbytes);
-        const auto vr = make_rsrc(vbase + static_cast<int64_t>(kb) * p.v_s, vbytes);
+        const auto kr = make_rsrc(kt, kbytes);
+        const auto vr = make_rsrc(vt, vbytes);
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int cidx = tid + i * NT;
@@ -465,21 +469,26 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
 
     // Query-tile-major grid, longest causal tiles first; with xcd_groups the
     // query heads of one KV head share blockIdx % 8, i.e. one XCD and its L2.
+    // Split-KV grids (packed sequences only): the splits of one query tile are
+    // adjacent blocks.
+    const int nsplit = VARLEN && p.n_splits > 1 ? p.n_splits : 1;
+    const int bid = static_cast<int>(blockIdx.x) / nsplit;
+    const int split = static_cast<int>(blockIdx.x) - bid * nsplit;
     int b, head, qo;
     if (p.seq_major) {
         // Sequence-major (unmasked or packed grids): the blocks of one sequence
         // run together and share its K/V tiles in L2; the query heads of one KV
         // head keep one XCD when Hk is a multiple of 8.
         const int per_seq = p.q_blocks * p.heads;
-        b = blockIdx.x / per_seq;
-        const int rem = blockIdx.x - b * per_seq;
+        b = bid / per_seq;
+        const int rem = bid - b * per_seq;
         qo = rem / p.heads;
         const int idx = rem - qo * p.heads;
         head = (idx % p.kv_heads) * p.gqa + idx / p.kv_heads;
     } else {
         const int per_tile = p.batch * p.heads;
-        qo = blockIdx.x / per_tile;
-        const int rem = blockIdx.x - qo * per_tile;
+        qo = bid / per_tile;
+        const int rem = bid - qo * per_tile;
         int bh;
         if (p.xcd_groups) {
             const int xcd = rem & 7;
@@ -504,22 +513,16 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     int64_t q_off = 0, k_off = 0;
     int sq = p.seqlen_q, sk = p.seqlen_k;
     int lse_row0 = 0;
+    int64_t k_batch = 0;
     if constexpr (VARLEN) {
-        const int qs = p.cu_q[b];
-        const int qe = p.cu_q[b + 1];
-        const int ks = p.cu_k[b];
-        const int ke = p.cu_k[b + 1];
-        const int len = p.seqused_k ? p.seqused_k[b] : ke - ks;
-        const int pad = p.leftpad_k ? p.leftpad_k[b] : 0;
-        if (qs < 0 || qe < qs || qe > p.total_q || ks < 0 || ke < ks || ke > p.total_k || pad < 0 ||
-            len < pad || len > ke - ks || qe - qs > p.seqlen_q) {
-            return;
-        }
-        sq = qe - qs;
-        sk = len - pad;
-        q_off = static_cast<int64_t>(qs);
-        k_off = static_cast<int64_t>(ks + pad);
-        lse_row0 = qs;
+        const VarSeq vs = varlen_seq(p, b);
+        if (!vs.ok) return;
+        sq = vs.sq;
+        sk = vs.sk;
+        q_off = static_cast<int64_t>(vs.qs);
+        k_off = vs.k_row0;
+        k_batch = vs.k_batch;
+        lse_row0 = vs.qs;
         qb = (sq + BM - 1) / BM - 1 - qo;
         if (qb < 0) return;
     }
@@ -535,8 +538,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     uint16_t* obase;
     if constexpr (VARLEN) {
         qbase = static_cast<const uint16_t*>(p.q) + q_off * p.q_s + head * p.q_h;
-        kbase = static_cast<const uint16_t*>(p.k) + k_off * p.k_s + kvh * p.k_h;
-        vbase = static_cast<const uint16_t*>(p.v) + k_off * p.v_s + kvh * p.v_h;
+        kbase = static_cast<const uint16_t*>(p.k) + k_batch * p.k_b + k_off * p.k_s + kvh * p.k_h;
+        vbase = static_cast<const uint16_t*>(p.v) + k_batch * p.v_b + k_off * p.v_s + kvh * p.v_h;
         obase = static_cast<uint16_t*>(p.o) + q_off * p.o_s + head * p.o_h;
     } else {
         qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
@@ -567,13 +570,30 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     float m = -INFINITY, l = 0.0f;
 
     auto copy_tile = [&](int kb, int stage) {
-        copy_rows_dma<D, NW, BN>(kbase + static_cast<int64_t>(kb) * p.k_s, p.k_s, sk - kb, k_lds + stage * TILE,
-                             wave, lane);
-        copy_rows_dma<D, NW, BN>(vbase + static_cast<int64_t>(kb) * p.v_s, p.v_s, sk - kb, v_lds + stage * TILE,
-                             wave, lane);
+        const uint16_t* kt = kbase + static_cast<int64_t>(kb) * p.k_s;
+        const uint16_t* vt = vbase + static_cast<int64_t>(kb) * p.v_s;
+        int rows = sk - kb;
+        if constexpr (VARLEN) {
+            if (p.block_table) {
+                const int64_t page = page_of(p, b, kb);
+                const int64_t within = kb % p.page_size;
+                kt = kbase + page * p.k_page + within * p.k_s;
+                vt = vbase + page * p.v_page + within * p.v_s;
+                if (page < 0) rows = 0;
+            }
+        }
+        copy_rows_dma<D, NW, BN>(kt, p.k_s, rows, k_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, BN>(vt, p.v_s, rows, v_lds + stage * TILE, wave, lane);
     };
 
-    const int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
+    int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
+    if (nsplit > 1) {
+        // This split's share of the key tiles (possibly none).
+        const int per = (ntiles + nsplit - 1) / nsplit;
+        const int lo = min(ntiles, split * per);
+        kv_begin += lo * BN;
+        ntiles = min(ntiles, lo + per) - lo;
+    }
     if (ntiles > 0) {
         copy_tile(kv_begin, 0);
         wait_vmem();
@@ -693,6 +713,26 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     }
 
     const float lt = l + __shfl_xor(l, 32, 64);
+    if (nsplit > 1) {
+        // fp32 partials of this split: O normalised by its own row sum, LSE
+        // -inf when the split saw no key of the row.
+        if (row < sq) {
+            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+            const int64_t prow = (static_cast<int64_t>(split) * p.heads + head) * p.total_q + lse_row0 + row;
+            float* op = p.o_part + prow * D;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * db + 8 * g + 4 * hh;
+                    *reinterpret_cast<float4*>(op + d) = float4{o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
+                                                                o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+                }
+            }
+            if (hh == 0) p.lse_part[prow] = lt > 0.0f ? (m + fast_log2(lt)) * kLn2 : -INFINITY;
+        }
+        return;
+    }
     if (row < sq) {
         const float inv = (lt > 0.0f ? 1.0f / lt : 0.0f) * (DROPOUT ? p.inv_keep : 1.0f);
         uint16_t* orow = obase + row * p.o_s;
@@ -1022,6 +1062,49 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
     }
 }
 
+// Split-KV merge (flash-attn2-rs/src/device/varlen/merge.rs): per row,
+// LSE = log sum_i exp(LSE_i) and O = sum_i exp(LSE_i - LSE) O_i over the splits;
+// a row no split saw gets O = 0 and LSE = +inf, as an empty row does. One wave
+// per (head, packed row); lane l < D / 2 owns columns 2l and 2l + 1.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restrict__ o_part,
+                                                           const float* __restrict__ lse_part, int n_splits,
+                                                           int heads, int total_q, uint16_t* __restrict__ o,
+                                                           int64_t o_s, int64_t o_h, float* __restrict__ lse,
+                                                           int64_t lse_h) {
+    static_assert(D % 2 == 0 && D <= 128, "two columns per lane");
+    constexpr int PER = 2;
+    const int lane = threadIdx.x & 63;
+    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= static_cast<int64_t>(heads) * total_q) return;
+    const int head = static_cast<int>(item / total_q);
+    const int row = static_cast<int>(item - static_cast<int64_t>(head) * total_q);
+    const int64_t stride = static_cast<int64_t>(heads) * total_q;  // between splits
+    float mx = -INFINITY;
+    for (int i = 0; i < n_splits; ++i) mx = fmaxf(mx, lse_part[i * stride + item]);
+    float acc[PER] = {};
+    float out_lse = INFINITY;
+    if (mx > -INFINITY) {
+        float sum = 0.0f;
+        for (int i = 0; i < n_splits; ++i) sum += expf(lse_part[i * stride + item] - mx);
+        out_lse = mx + logf(sum);
+        for (int i = 0; i < n_splits; ++i) {
+            const float w = expf(lse_part[i * stride + item] - out_lse);
+            if (w == 0.0f) continue;
+            if (lane < D / 2) {
+                const float* src = o_part + (i * stride + item) * D + PER * lane;
+                acc[0] += w * src[0];
+                acc[1] += w * src[1];
+            }
+        }
+    }
+    if (lane < D / 2) {
+        uint16_t* dst = o + static_cast<int64_t>(row) * o_s + static_cast<int64_t>(head) * o_h + PER * lane;
+        *reinterpret_cast<uint32_t*>(dst) = pack2<T>(acc[0], acc[1]);
+    }
+    if (lane == 0) lse[static_cast<int64_t>(head) * lse_h + row] = out_lse;
+}
+
 // Empty-key rows: O = 0, LSE = +inf (host/forward/mod.rs:548-572). Also clears
 // the output when zero_tensors is requested. Uses kernels rather than
 // hipMemsetAsync so the calls stay safe inside captured graphs.
@@ -1093,7 +1176,8 @@ template <typename T, int D, bool VARLEN>
 void launch_tiled(FwdParams& prm, hipStream_t s) {
     constexpr int BM = 128;
     prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
-    const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads;
+    const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads *
+                           (VARLEN && prm.n_splits > 1 ? prm.n_splits : 1);
     if (blocks == 0) return;
     if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
     prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
@@ -1414,5 +1498,182 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<true>(prm, q->dtype, bucket_for(D), general, s);
+    });
+}
+
+// Split-KV scratch: fp32 partial O [n_splits, H, Tq, D] and LSE [n_splits, H, Tq].
+extern "C" int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int64_t heads, int64_t total_q,
+                                                         int64_t head_dim) {
+    if (num_splits <= 1 || heads <= 0 || total_q <= 0 || head_dim <= 0) return 0;
+    const int64_t d = bucket_for(head_dim);
+    return num_splits * heads * total_q * (d + 1) * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
+                                     const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k,
+                                     const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                                     const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
+                                     double scale, int causal, int64_t window_left, int64_t window_right,
+                                     double softcap, int64_t max_seqlen_q, int64_t num_splits, void* workspace,
+                                     int64_t workspace_bytes, const kcr_tensor* out, const kcr_tensor* lse,
+                                     void* stream) {
+    return guarded([&] {
+        check_qkv(q, "q", 3);
+        check_qkv(kcache, "kcache", 4);
+        check_qkv(vcache, "vcache", 4);
+        if (kcache->dtype != q->dtype || vcache->dtype != q->dtype) {
+            throw type_error("q, kcache and vcache must share dtype (all f16 or all bf16)");
+        }
+        if (shape_of(*kcache) != shape_of(*vcache)) throw value_error("K/V cache shapes must match");
+        if (!cu_seqlens_q || cu_seqlens_q->ndim != 1 || cu_seqlens_q->shape[0] < 2) {
+            throw value_error("cu_seqlens_q must have shape [batch + 1]");
+        }
+        const int64_t batch = cu_seqlens_q->shape[0] - 1;
+        const int64_t Tq = q->shape[0], H = q->shape[1], D = q->shape[2];
+        const int64_t Bc = kcache->shape[0], S = kcache->shape[1], Hk = kcache->shape[2];
+        check_head_dim(D);
+        if (kcache->shape[3] != D) throw value_error("K/V cache shapes must match Q's head size");
+        if (batch <= 0 || batch > 65535 || H <= 0 || H > 65535 || Hk <= 0 || H % Hk != 0 || Tq > INT32_MAX ||
+            max_seqlen_q < 0 || max_seqlen_q > INT32_MAX - 256 || Bc <= 0 || S <= 0) {
+            throw value_error("unsupported cached attention dimensions");
+        }
+        auto check_meta = [&](const kcr_tensor* t, std::vector<int64_t> shape, const char* name) {
+            if (!t) return;
+            if (t->dtype != KCR_INT32 || shape_of(*t) != shape || t->strides[t->ndim - 1] != 1 ||
+                (t->ndim == 1 && !is_contiguous(*t))) {
+                throw value_error(std::string(name) + " must be int32 " + shape_string(shape) +
+                                  " with unit last stride");
+            }
+            require_device(t, name);
+        };
+        if (!seqused_k) throw value_error("seqused_k (cache lengths after the append) is required");
+        check_meta(cu_seqlens_q, {batch + 1}, "cu_seqlens_q");
+        check_meta(seqused_k, {batch}, "seqused_k");
+        check_meta(leftpad_k, {batch}, "leftpad_k");
+        check_meta(cache_batch_idx, {batch}, "cache_batch_idx");
+        int64_t capacity = S;
+        if (block_table) {
+            if (block_table->ndim != 2) throw value_error("block_table must be int32 [batch, max_blocks]");
+            check_meta(block_table, {batch, block_table->shape[1]}, "block_table");
+            if (S % 256 != 0 || leftpad_k || cache_batch_idx) {
+                throw value_error("paged caches require page size divisible by 256 and no leftpad or cache_batch_idx");
+            }
+            capacity = S * block_table->shape[1];
+            if (block_table->strides[0] < 0 || block_table->strides[0] > INT32_MAX) {
+                throw value_error("block_table row stride must fit int32");
+            }
+        }
+        if (capacity > INT32_MAX - 256 || Bc * S > INT32_MAX) throw value_error("cache/query dimensions must fit int32");
+        int32_t alibi_b = 0;
+        check_alibi(alibi, batch, H, alibi_b);
+        if (!out || shape_of(*out) != shape_of(*q) || out->dtype != q->dtype || out->strides[2] != 1) {
+            throw value_error("out must match q's shape and dtype with unit last stride");
+        }
+        if (!lse || lse->dtype != KCR_FLOAT32 || lse->ndim != 2 || lse->shape[0] != H || lse->shape[1] != Tq ||
+            !is_contiguous(*lse)) {
+            throw value_error("lse must be contiguous float32 [H, total_q]");
+        }
+        for (auto* t : {q, kcache, vcache, out}) {
+            if (Tq > 0 && !rows_aligned16(t)) {
+                throw value_error("q, caches and out must have 16-byte aligned rows (strides multiple of 8 elements)");
+            }
+        }
+        check_kv_rows(kcache, vcache, 1, D);
+        for (auto* t : {q, kcache, vcache, out, lse}) require_device(t, "tensor");
+        if (num_splits < 0 || num_splits > 128) throw value_error("num_splits must be in 0..=128");
+        auto s = static_cast<hipStream_t>(stream);
+        const Options opt = normalize_options(has_scale, scale, causal, window_left, window_right, softcap, D,
+                                              capacity);
+        if (Tq == 0 || max_seqlen_q == 0) return;
+        FwdParams prm{};
+        prm.q = q->data;
+        prm.k = kcache->data;
+        prm.v = vcache->data;
+        prm.o = out->data;
+        prm.lse = static_cast<float*>(lse->data);
+        prm.alibi = alibi ? static_cast<const float*>(alibi->data) : nullptr;
+        prm.cu_q = static_cast<const int32_t*>(cu_seqlens_q->data);
+        prm.seqused_k = static_cast<const int32_t*>(seqused_k->data);
+        prm.leftpad_k = leftpad_k ? static_cast<const int32_t*>(leftpad_k->data) : nullptr;
+        prm.total_q = static_cast<int32_t>(Tq);
+        prm.q_s = q->strides[0]; prm.q_h = q->strides[1];
+        prm.k_b = kcache->strides[0]; prm.k_s = kcache->strides[1]; prm.k_h = kcache->strides[2];
+        prm.v_b = vcache->strides[0]; prm.v_s = vcache->strides[1]; prm.v_h = vcache->strides[2];
+        prm.o_s = out->strides[0]; prm.o_h = out->strides[1];
+        prm.lse_b = 0;
+        prm.lse_h = Tq;
+        prm.batch = static_cast<int32_t>(batch);
+        prm.heads = static_cast<int32_t>(H);
+        prm.kv_heads = static_cast<int32_t>(Hk);
+        prm.gqa = static_cast<int32_t>(H / Hk);
+        prm.seqlen_q = static_cast<int32_t>(max_seqlen_q);
+        prm.seqlen_k = static_cast<int32_t>(capacity);
+        prm.head_dim = static_cast<int32_t>(D);
+        prm.window_left = opt.window_left;
+        prm.window_right = opt.window_right;
+        prm.alibi_b = alibi_b;
+        prm.alibi_causal = opt.alibi_causal;
+        prm.scale_log2 = opt.scale * kLog2e;
+        prm.tanh_scale = opt.tanh_scale;
+        prm.scale_eff_log2 = opt.scale_eff * kLog2e;
+        prm.drop_threshold = 255;
+        prm.inv_keep = 1.0f;
+        prm.cache_mode = 1;
+        prm.capacity = static_cast<int32_t>(capacity);
+        prm.cache_batches = static_cast<int32_t>(Bc);
+        prm.cache_idx = cache_batch_idx ? static_cast<const int32_t*>(cache_batch_idx->data) : nullptr;
+        if (block_table) {
+            prm.block_table = static_cast<const int32_t*>(block_table->data);
+            prm.table_stride = block_table->strides[0];
+            prm.table_cols = static_cast<int32_t>(block_table->shape[1]);
+            prm.page_size = static_cast<int32_t>(S);
+            prm.k_page = kcache->strides[0];
+            prm.v_page = vcache->strides[0];
+        }
+        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
+        const int bucket = bucket_for(D);
+        const bool tiled = !general && (bucket == 64 || bucket == 128);
+        if (block_table && !tiled) {
+            throw value_error("paged caches support head size 64 or 128 without softcap or ALiBi");
+        }
+        const int64_t splits = tiled ? std::max<int64_t>(1, num_splits) : 1;
+        if (splits > 1) {
+            const int64_t need = kcr_flash_fwd_kvcache_workspace_bytes(splits, H, Tq, D);
+            if (!workspace || workspace_bytes < need) {
+                throw value_error("workspace must hold " + std::to_string(need) + " bytes for " +
+                                  std::to_string(splits) + " splits");
+            }
+            if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) throw value_error("workspace must be 16-byte aligned");
+            prm.n_splits = static_cast<int32_t>(splits);
+            prm.o_part = static_cast<float*>(workspace);
+            prm.lse_part = prm.o_part + splits * H * Tq * bucket;
+            // Splits that see no row of an invalid sequence leave LSE -inf.
+            fill_f32(prm.lse_part, splits * H * Tq, -INFINITY, s);
+        }
+        launch_fwd<true>(prm, q->dtype, bucket, general, s);
+        if (splits > 1) {
+            const int64_t items = H * Tq;
+            const unsigned grid = static_cast<unsigned>((items + 3) / 4);
+            auto merge = [&](auto tag) {
+                using T = decltype(tag);
+                if (bucket == 64) {
+                    merge_splits_kernel<T, 64><<<grid, 256, 0, s>>>(prm.o_part, prm.lse_part, prm.n_splits,
+                                                                    prm.heads, prm.total_q,
+                                                                    static_cast<uint16_t*>(prm.o), prm.o_s,
+                                                                    prm.o_h, prm.lse, prm.lse_h);
+                } else {
+                    merge_splits_kernel<T, 128><<<grid, 256, 0, s>>>(prm.o_part, prm.lse_part, prm.n_splits,
+                                                                     prm.heads, prm.total_q,
+                                                                     static_cast<uint16_t*>(prm.o), prm.o_s,
+                                                                     prm.o_h, prm.lse, prm.lse_h);
+                }
+            };
+            if (q->dtype == KCR_BFLOAT16) {
+                merge(bf16_t{});
+            } else {
+                merge(f16_t{});
+            }
+            check_launch("launch merge_splits");
+        }
     });
 }

@@ -1,8 +1,7 @@
 """flash-attn2-rs on MI355X: FlashAttention-2 forward (dense, varlen) and backward.
 
-Mirrors flash-attn2-rs/tvm-ffi-ext/flash_attn2_rs/__init__.py. The KV-cache
-entry points (fwd_kvcache, flash_attn_with_kvcache) and dropout are not part of
-this build.
+Mirrors flash-attn2-rs/tvm-ffi-ext/flash_attn2_rs/__init__.py, including the
+KV-cache entry points (ops.fwd_kvcache, flash_attn_with_kvcache) and dropout.
 """
 
 from ._ops import ops
@@ -14,6 +13,7 @@ from .flash_attn_interface import (
     flash_attn_varlen_func,
     flash_attn_varlen_kvpacked_func,
     flash_attn_varlen_qkvpacked_func,
+    flash_attn_with_kvcache,
     fwd,
     fwd_explicit,
     varlen_bwd,
@@ -34,4 +34,5 @@ __all__ = [
     "flash_attn_varlen_func",
     "flash_attn_varlen_qkvpacked_func",
     "flash_attn_varlen_kvpacked_func",
+    "flash_attn_with_kvcache",
 ]

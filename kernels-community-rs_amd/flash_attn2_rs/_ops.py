@@ -14,6 +14,12 @@ positional signatures and return conventions, backed by libkcr_hip.so.
   varlen_bwd_explicit(q, k, v, dout, out, lse, cuq, cuk, alibi, scale, causal, left,
       right, softcap, p, state, max_q, max_k, zero_tensors) -> [dq, dk, dv, delta]
                                              host/varlen/backward.rs:15-546
+  fwd_kvcache(q, kcache, vcache, k, v, seqlens_k, rotary_cos, rotary_sin,
+      cache_batch_idx, leftpad_k, block_table, alibi_slopes, out, softmax_scale,
+      is_causal, window_size_left, window_size_right, softcap,
+      is_rotary_interleaved, num_splits) -> [out, lse]
+                                             flash_attn_interface.py:1474-1700,
+                                             host/cache/mod.rs:36-320
 
 Outputs the reference allocates with `TVMFFIEnvTensorAlloc` are allocated here with
 torch's allocator (the same allocator tvm-ffi forwards to under torch). Inputs
@@ -252,6 +258,117 @@ def varlen_bwd_explicit(q, k, v, dout, out, lse, cu_seqlens_q, cu_seqlens_k, ali
     return [dq, dk, dv, delta]
 
 
+def _auto_splits(blocks, key_tiles, device):
+    """Key splits for an underfilled grid (decode): enough blocks for two per CU,
+    at least 4 key tiles per split, at most 128 splits (host/varlen/mod.rs:673)."""
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    if blocks >= 2 * cus or key_tiles < 8:
+        return 1
+    return int(max(1, min(128, (2 * cus + blocks - 1) // blocks, key_tiles // 4)))
+
+
+def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=None, rotary_sin=None,
+                cache_batch_idx=None, leftpad_k=None, block_table=None, alibi_slopes=None, out=None,
+                softmax_scale=None, is_causal=False, window_size_left=-1, window_size_right=-1,
+                softcap=0.0, is_rotary_interleaved=False, num_splits=1):
+    """Cached inference (flash_attn_interface.py:1474-1700): appends new K/V at
+    positions seqlens_k[b] .. (rotating K, and Q, when rotary tables are given),
+    then attends over cache rows [leftpad_k[b], seqlens_k[b] + new). Returns
+    [out [B, Sq, H, D], lse [B, H, Sq]]. Decode steps (Sq = 1) with GQA treat the
+    query heads of a KV head as query rows, as the reference does."""
+    for name, t in (("q", q), ("kcache", kcache), ("vcache", vcache)):
+        if not isinstance(t, torch.Tensor) or t.ndim != 4:
+            raise RuntimeError(f"{name} must be rank 4")
+    b, sq, h, d = q.shape
+    if not 0 < d <= 256:
+        raise RuntimeError("head size must be in 1..256")
+    if kcache.shape != vcache.shape or kcache.shape[-1] != d:
+        raise RuntimeError("K/V cache shapes must match Q's head size")
+    if any(t.stride(-1) != 1 for t in (q, kcache, vcache)):
+        raise RuntimeError("Input tensor must have contiguous last dimension")
+    if d % 8:
+        raise ValueError("head_size must be a positive multiple of 8 in this build")
+    splits = int(num_splits)
+    if not splits <= 128:
+        raise RuntimeError("num_splits must fit int32 and be at most 128")
+    left, right = int(window_size_left), int(window_size_right)
+    hk = kcache.shape[2]
+    if block_table is not None:
+        if block_table.ndim != 2 or block_table.shape[0] != b or block_table.dtype != torch.int32:
+            raise RuntimeError("block_table must be int32 [batch, max_blocks] with unit last stride on Q's device")
+        if kcache.shape[1] % 256 or leftpad_k is not None or cache_batch_idx is not None:
+            raise RuntimeError("paged caches require page size divisible by 256 and no leftpad or cache_batch_idx")
+        capacity = kcache.shape[1] * block_table.shape[1]
+    else:
+        capacity = kcache.shape[1]
+        if cache_batch_idx is None and kcache.shape[0] < b:
+            raise RuntimeError("cache batch is too small for Q")
+    if cache_batch_idx is not None and cache_batch_idx.shape != (b,):
+        cache_batch_idx = cache_batch_idx.reshape(-1)[:b]
+    if k is None and v is not None and not isinstance(v, torch.Tensor):
+        raise RuntimeError("v must be a Tensor or None")
+    if k is not None and v is None:
+        raise RuntimeError("new V is required when new K is supplied")
+    if (rotary_cos is None) != (rotary_sin is None):
+        raise RuntimeError("rotary sin is required when rotary cos is supplied")
+    if rotary_cos is not None and k is None:
+        raise RuntimeError("rotary tables require new K/V")
+    new_keys = 0 if k is None else k.shape[1]
+    if new_keys > 0 and seqlens_k is None:
+        raise RuntimeError("cache lengths are required when appending K/V")
+    if new_keys > 0 and (k.shape != v.shape or new_keys > capacity):
+        raise RuntimeError("new K/V shapes must match and fit the cache capacity")
+    causal = bool(is_causal)
+    if new_keys > 0:
+        rotated = torch.empty_like(q) if rotary_cos is not None else None
+        advance_q = causal or 0 <= left < capacity or 0 <= right < capacity
+        call("kcr_flash_cache_update", *(ref(describe(t)) for t in (
+                 q, kcache, vcache, k, v, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx, block_table)),
+             int(bool(is_rotary_interleaved)), int(advance_q), ref(describe(rotated)), stream_of(q))
+        if rotated is not None:
+            q = rotated
+    # Cache rows attended: [leftpad, seqlens_k + new) (all rows without lengths).
+    if seqlens_k is None:
+        used = torch.full((b,), capacity, dtype=torch.int32, device=q.device)
+    else:
+        used = (seqlens_k.to(torch.int32) + new_keys).contiguous()
+    grouped = sq == 1 and h > hk and left < 0 and right < 0 and alibi_slopes is None
+    if grouped:
+        g = h // hk
+        qp = q.reshape(b, hk, g, d).transpose(1, 2).reshape(b * g, hk, d).contiguous()
+        rows, heads = g, hk
+        causal = False  # one query row sees every key either way
+    else:
+        qp = q.reshape(b * sq, h, d)
+        if qp.stride(-1) != 1 or not _rows_aligned(qp):
+            qp = qp.contiguous()
+        rows, heads = sq, h
+    cu_q = torch.arange(0, (b + 1) * rows, rows, dtype=torch.int32, device=q.device)
+    out_p = torch.empty((b * rows, heads, d), dtype=q.dtype, device=q.device)
+    lse_p = torch.empty((heads, b * rows), dtype=torch.float32, device=q.device)
+    if splits < 1:
+        splits = _auto_splits(b * heads * ((rows + 127) // 128), (capacity + 63) // 64, q.device)
+    ws_bytes = lib.kcr_flash_fwd_kvcache_workspace_bytes(splits, heads, b * rows, d)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    has_scale, sc = _scale_args(softmax_scale)
+    call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (
+             qp, kcache, vcache, cu_q, used, leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
+         has_scale, sc, int(causal), ctypes.c_int64(left), ctypes.c_int64(right),
+         ctypes.c_double(float(softcap)), ctypes.c_int64(rows), ctypes.c_int64(splits),
+         ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), ref(describe(out_p)),
+         ref(describe(lse_p)), stream_of(q))
+    if grouped:
+        output = out_p.reshape(b, g, hk, d).transpose(1, 2).reshape(b, 1, h, d)
+        lse = lse_p.reshape(hk, b, g).permute(1, 0, 2).reshape(b, h, 1)
+    else:
+        output = out_p.reshape(b, sq, h, d)
+        lse = lse_p.reshape(h, b, sq).permute(1, 0, 2)
+    if out is not None:
+        out.copy_(output)
+        output = out
+    return [output, lse.contiguous()]
+
+
 ops = SimpleNamespace(
     fwd=fwd,
     fwd_lse=fwd_lse,
@@ -261,4 +378,5 @@ ops = SimpleNamespace(
     bwd_dkv=bwd_dkv,
     bwd_all=bwd_all,
     varlen_bwd_explicit=varlen_bwd_explicit,
+    fwd_kvcache=fwd_kvcache,
 )

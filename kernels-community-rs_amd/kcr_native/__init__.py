@@ -86,7 +86,8 @@ def _load():
     lib = ctypes.CDLL(str(LIB_PATH))
     lib.kcr_last_error.restype = ctypes.c_char_p
     lib.kcr_version.restype = ctypes.c_char_p
-    for name in ("kcr_flash_bwd_workspace_bytes", "kcr_flash_varlen_bwd_workspace_bytes"):
+    for name in ("kcr_flash_bwd_workspace_bytes", "kcr_flash_varlen_bwd_workspace_bytes",
+                 "kcr_flash_fwd_kvcache_workspace_bytes"):
         if hasattr(lib, name):
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int64
