@@ -193,6 +193,31 @@ def _wl_fa_varlen(kind):
     return make
 
 
+def wl_fa_kvcache_decode():
+    """flash_attn_with_kvcache decode step (no BASELINE config):
+    B=16 sequences with 8191 cached tokens each, one new token appended, Hq=32,
+    Hkv=8, D=128 bf16, causal, automatic key splits. HBM-bound: the step reads the
+    whole K/V cache once, 16 x 8192 x 8 x 128 x 2 x 2 = 536,870,912 B."""
+    import flash_attn2_rs
+
+    b, hq, hkv, d, cap = 16, 32, 8, 128, 8192
+    g = _gen(7)
+    kc = torch.randn(b, cap, hkv, d, generator=g).bfloat16().cuda()
+    vc = torch.randn(b, cap, hkv, d, generator=g).bfloat16().cuda()
+    q = torch.randn(b, 1, hq, d, generator=g).bfloat16().cuda()
+    kn = torch.randn(b, 1, hkv, d, generator=g).bfloat16().cuda()
+    vn = torch.randn(b, 1, hkv, d, generator=g).bfloat16().cuda()
+    lengths = torch.full((b,), cap - 1, dtype=torch.int32, device="cuda")
+
+    def run():
+        flash_attn2_rs.flash_attn_with_kvcache(q, kc, vc, kn, vn, cache_seqlens=lengths, causal=True,
+                                               num_splits=0)
+
+    return dict(run=run, work=2 * b * cap * hkv * d * 2, bound="hbm", kernel="flash_fwd_tiled",
+                config={"B": b, "Hq": hq, "Hkv": hkv, "D": d, "cache_len": cap, "new_tokens": 1,
+                        "causal": True, "dtype": "bf16"}, cpu=None)
+
+
 def wl_hbm_copy():
     """Plain device copy of the activation input size (939,524,096 B read and
     written): the known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE
@@ -221,6 +246,7 @@ WORKLOADS = {
     "silu_and_mul": _wl_gated("silu_and_mul"),
     "gelu_and_mul": _wl_gated("gelu_and_mul"),
     "gelu_tanh_and_mul": _wl_gated("gelu_tanh_and_mul"),
+    "fa_kvcache_decode": wl_fa_kvcache_decode,
     "hbm_copy": wl_hbm_copy,
 }
 DEFAULT_ORDER = [n for n in WORKLOADS if n != "hbm_copy"]
