@@ -138,7 +138,8 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
                         causal, left, right, softcap, p, state, max_q, max_k, return_softmax,
                         zero_tensors, block_table=None):
     if block_table is not None:
-        raise NotImplementedError("paged K/V (block_table) is not supported by this build")
+        return _paged_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi, scale,
+                                 causal, left, right, softcap, p, max_q, return_softmax, block_table)
     # host/varlen/mod.rs:201-229
     p = float(p)
     if (not (p == p) or not 0.0 <= p < 1.0 or float(np.float32(p)) >= 1.0
@@ -164,6 +165,30 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
          ref(describe(out)), ref(describe(lse)), stream_of(q))
     probabilities = torch.empty(0, dtype=q.dtype, device=q.device)
     return [out, lse, probabilities]
+
+
+def _paged_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi, scale, causal,
+                      left, right, softcap, p, max_q, return_softmax, block_table):
+    """varlen_fwd_explicit with a block table (host/varlen/mod.rs:36-54, arg 19):
+    k/v are pages [num_pages, page_size, Hk, D]; sequence b reads its first
+    seqused_k[b] (or cu_seqlens_k[b + 1] - cu_seqlens_k[b]) keys through
+    block_table[b, :]."""
+    if float(np.float32(float(p))) > 0.0 or return_softmax:
+        raise ValueError("paged K/V does not support dropout or returned probabilities")
+    if leftpad_k is not None:
+        raise ValueError("paged caches require page size divisible by 256 and no leftpad or cache_batch_idx")
+    if seqused_k is None:
+        seqused_k = (cu_seqlens_k[1:] - cu_seqlens_k[:-1]).to(torch.int32).contiguous()
+    qp = _packed(q)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
+    has_scale, sc = _scale_args(scale)
+    call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (
+             qp, k, v, cu_seqlens_q, seqused_k, None, None, block_table, alibi)),
+         has_scale, sc, int(bool(causal)), ctypes.c_int64(int(left)), ctypes.c_int64(int(right)),
+         ctypes.c_double(float(softcap)), ctypes.c_int64(int(max_q)), ctypes.c_int64(1),
+         ctypes.c_void_p(0), ctypes.c_int64(0), ref(describe(out)), ref(describe(lse)), stream_of(q))
+    return [out, lse, torch.empty(0, dtype=q.dtype, device=q.device)]
 
 
 def bwd_preprocess(dout, out, p):

@@ -10,6 +10,7 @@ from typing import Optional, Tuple
 
 import torch
 
+from ._ops import ops
 from ._ops import torch_add_op_namespace_prefix as add_op_namespace_prefix
 from .flash_attn_interface import bwd, fwd, varlen_bwd, varlen_fwd
 
@@ -152,8 +153,21 @@ class _VarlenAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, cuq, cuk, max_q, max_k, dropout_p, softmax_scale, causal,
                 window_size, softcap, slopes, deterministic, return_probs, block_table, packing):
+        ctx.paged = block_table is not None
         if block_table is not None:
-            raise NotImplementedError("paged K/V (block_table) is not supported by this build")
+            # Paged K/V [pages, page_size, Hk, D]: inference only (no backward).
+            if float(dropout_p) > 0.0:
+                raise ValueError("paged K/V does not support dropout")
+            if q.ndim != 3 or k.ndim != 4 or v.ndim != 4:
+                raise ValueError("q must be rank 3; k/v must be rank 4 with block_table, otherwise rank 3")
+            left, right = window_size
+            cuk = cuq if cuk is None else cuk
+            out, lse, _ = ops.varlen_fwd_explicit(q, k, v, cuq, cuk, None, None, slopes, softmax_scale,
+                                                  causal, left, right, softcap, 0.0, None, max_q, max_k,
+                                                  False, False, block_table)
+            if return_probs:
+                return out, lse, torch.empty(0, device=q.device, dtype=q.dtype)
+            return out
         if cuk is None:
             cuk = cuq
         if packing == 3:
@@ -187,6 +201,8 @@ class _VarlenAttention(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, dout, *unused):
+        if ctx.paged:
+            raise RuntimeError("paged K/V (block_table) attention has no backward")
         q, k, v, out, lse, cuq, cuk, slopes, rng_state = ctx.saved_tensors
         max_q, max_k, scale, causal, left, right, cap, dropout_p = ctx.options
         (dout,) = _pad(ctx.dim, dout)

@@ -194,7 +194,17 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, le
     if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
         _cpu_dispatch("varlen_fwd")
     if block_table is not None:
-        raise NotImplementedError("paged K/V (block_table) is not supported by this build")
+        # Paged K/V [pages, page_size, Hk, D] (interface.py:1012-1241 with a block table).
+        if softmax_scale is None:
+            softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
+        output, lse, probabilities = ops.varlen_fwd_explicit(
+            q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi_slopes, float(softmax_scale),
+            bool(is_causal), int(window_size_left), int(window_size_right), float(softcap), float(p_dropout),
+            None, int(max_seqlen_q), int(max_seqlen_k), bool(return_softmax), bool(zero_tensors), block_table)
+        if out is not None:
+            out.copy_(output)
+            output = out
+        return [output, lse, probabilities, torch.empty(2, device=q.device, dtype=torch.int64)]
     p = _check_dropout(p_dropout, softcap)
     _check_return_softmax(return_softmax, p)
     _validate(q, k, v, out, alibi_slopes, softcap, packed=True)

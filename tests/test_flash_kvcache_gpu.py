@@ -189,3 +189,29 @@ def test_split_merge_matches_unsplit():
         got = _run(q, kc, vc, k, v, lengths, causal=True, splits=s)
         assert (got[0].float() - base[0].float()).abs().max() <= 1e-2
         assert (got[1] - base[1]).abs().max() <= 1e-4
+
+
+def test_paged_varlen_func_forward():
+    """flash_attn_varlen_func with a block table (paged K/V, forward only): packed
+    queries of 3 sequences over keys read through the table."""
+    import flash_attn2_rs
+
+    g = torch.Generator().manual_seed(13)
+    page, cols, Hk, H, D = 256, 2, 2, 4, 128
+    lens_q, lens_k = [5, 1, 64], [300, 17, 512]
+    B = len(lens_q)
+    kp = torch.randn(B * cols, page, Hk, D, generator=g).bfloat16()
+    vp = torch.randn(B * cols, page, Hk, D, generator=g).bfloat16()
+    q = torch.randn(sum(lens_q), H, D, generator=g).bfloat16()
+    table = np.random.default_rng(14).permutation(B * cols).reshape(B, cols).astype(np.int32)
+    cu_q = torch.tensor(np.cumsum([0] + lens_q), dtype=torch.int32)
+    cu_k = torch.tensor(np.cumsum([0] + lens_k), dtype=torch.int32)
+    out = flash_attn2_rs.flash_attn_varlen_func(
+        q.cuda(), kp.cuda(), vp.cuda(), cu_q.cuda(), cu_k.cuda(), max(lens_q), max(lens_k), causal=True,
+        block_table=torch.from_numpy(table).cuda())
+    torch.cuda.synchronize()
+    qs = np.cumsum([0] + lens_q)
+    for b in range(B):
+        qb = q[qs[b]:qs[b + 1]].float().numpy()[None]
+        eo, _ = KV.attend(qb, _f(kp), _f(vp), np.array([lens_k[b]]), block_table=table[b:b + 1], causal=True)
+        assert np.abs(out[qs[b]:qs[b + 1]].float().cpu().numpy() - eo[0]).max() <= 2e-2
