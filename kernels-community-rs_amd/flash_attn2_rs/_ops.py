@@ -33,6 +33,7 @@ the generator-descriptor arities are not part of this build.
 from __future__ import annotations
 
 import ctypes
+import math
 from types import SimpleNamespace
 
 import numpy as np
@@ -295,7 +296,7 @@ def _auto_splits(blocks, key_tiles, device):
 def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=None, rotary_sin=None,
                 cache_batch_idx=None, leftpad_k=None, block_table=None, alibi_slopes=None, out=None,
                 softmax_scale=None, is_causal=False, window_size_left=-1, window_size_right=-1,
-                softcap=0.0, is_rotary_interleaved=False, num_splits=1):
+                softcap=0.0, is_rotary_interleaved=False, num_splits=1, _caches_out=None):
     """Cached inference (flash_attn_interface.py:1474-1700): appends new K/V at
     positions seqlens_k[b] .. (rotating K, and Q, when rotary tables are given),
     then attends over cache rows [leftpad_k[b], seqlens_k[b] + new). Returns
@@ -311,8 +312,6 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
         raise RuntimeError("K/V cache shapes must match Q's head size")
     if any(t.stride(-1) != 1 for t in (q, kcache, vcache)):
         raise RuntimeError("Input tensor must have contiguous last dimension")
-    if d % 8:
-        raise ValueError("head_size must be a positive multiple of 8 in this build")
     splits = int(num_splits)
     if not splits <= 128:
         raise RuntimeError("num_splits must fit int32 and be at most 128")
@@ -338,11 +337,36 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
         raise RuntimeError("rotary sin is required when rotary cos is supplied")
     if rotary_cos is not None and k is None:
         raise RuntimeError("rotary tables require new K/V")
+    if k is not None:
+        # flash_attn_interface.py:600-631: checked before anything is written.
+        if seqlens_k is None:
+            raise RuntimeError("cache lengths are required when appending K/V")
+        for name, t in (("k", k), ("v", v)):
+            if (not isinstance(t, torch.Tensor) or t.ndim != 4 or t.shape[0] != b
+                    or t.shape[2:] != kcache.shape[2:] or t.dtype != q.dtype or t.device != q.device
+                    or t.stride(-1) != 1):
+                raise RuntimeError(
+                    f"{name} must match query batch and cache heads/dtype/device with unit last stride")
+        if k.shape != v.shape or k.shape[1] > capacity or sq > capacity:
+            raise RuntimeError("new K/V shapes must match and fit the cache capacity")
     new_keys = 0 if k is None else k.shape[1]
-    if new_keys > 0 and seqlens_k is None:
-        raise RuntimeError("cache lengths are required when appending K/V")
-    if new_keys > 0 and (k.shape != v.shape or new_keys > capacity):
-        raise RuntimeError("new K/V shapes must match and fit the cache capacity")
+    if d % 8:
+        # Head sizes that are not a multiple of 8 run on zero-padded copies; the
+        # appended rows are copied back into the caller's caches afterwards
+        # (flash_attn_interface.py:1562-1566, 1640-1642).
+        pd = (d + 7) // 8 * 8
+        pad = (lambda t: None if t is None else torch.nn.functional.pad(t, (0, pd - d)))
+        result = fwd_kvcache(pad(q), pad(kcache), pad(vcache), pad(k), pad(v), seqlens_k, rotary_cos,
+                             rotary_sin, cache_batch_idx, leftpad_k, block_table, alibi_slopes, None,
+                             1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale, is_causal,
+                             window_size_left, window_size_right, softcap, is_rotary_interleaved,
+                             num_splits, _caches_out=(kcache, vcache) if new_keys > 0 else None)
+        output, lse = result
+        output = output[..., :d]
+        if out is not None:
+            out.copy_(output)
+            output = out
+        return [output, lse]
     causal = bool(is_causal)
     if new_keys > 0:
         rotated = torch.empty_like(q) if rotary_cos is not None else None
@@ -352,6 +376,14 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
              int(bool(is_rotary_interleaved)), int(advance_q), ref(describe(rotated)), stream_of(q))
         if rotated is not None:
             q = rotated
+        if _caches_out is not None:
+            # Padded copies: write the appended rows back to the caller's caches.
+            _caches_out[0].copy_(kcache[..., :_caches_out[0].shape[-1]])
+            _caches_out[1].copy_(vcache[..., :_caches_out[1].shape[-1]])
+        else:
+            # Native writes bypass torch's in-place ops: bump the versions so
+            # autograd sees the caches changed.
+            torch.autograd.graph.increment_version((kcache, vcache))
     # Cache rows attended: [leftpad, seqlens_k + new) (all rows without lengths).
     if seqlens_k is None:
         used = torch.full((b,), capacity, dtype=torch.int32, device=q.device)

@@ -215,3 +215,79 @@ def test_paged_varlen_func_forward():
         qb = q[qs[b]:qs[b + 1]].float().numpy()[None]
         eo, _ = KV.attend(qb, _f(kp), _f(vp), np.array([lens_k[b]]), block_table=table[b:b + 1], causal=True)
         assert np.abs(out[qs[b]:qs[b + 1]].float().cpu().numpy() - eo[0]).max() <= 2e-2
+
+
+def test_rejected_append_preserves_cache():
+    """A rejected append (V of another dtype) raises before writing anything
+    (test_gold.py:655-672)."""
+    import flash_attn2_rs
+
+    q = torch.randn(1, 1, 1, 16, device="cuda", dtype=torch.float16)
+    kc = torch.randn(1, 4, 1, 16, device="cuda", dtype=q.dtype)
+    vc = torch.randn_like(kc)
+    saved = (kc.clone(), vc.clone(), kc._version, vc._version)
+    with pytest.raises(RuntimeError):
+        flash_attn2_rs.flash_attn_with_kvcache(q, kc, vc, k=q, v=q.float(), cache_seqlens=1)
+    assert torch.equal(kc, saved[0]) and torch.equal(vc, saved[1])
+    assert (kc._version, vc._version) == saved[2:]
+
+
+def test_append_bumps_cache_versions():
+    """Native cache writes bump the tensors' versions, so a graph that saved the
+    old cache fails in backward (test_gold.py:675-689)."""
+    import flash_attn2_rs
+
+    q = torch.randn(1, 1, 1, 16, device="cuda", dtype=torch.float16)
+    kc = torch.randn(1, 4, 1, 16, device="cuda", dtype=q.dtype, requires_grad=True)
+    vc = torch.randn_like(kc, requires_grad=True)
+    loss = kc.square().float().sum() + vc.square().float().sum()
+    versions = (kc._version, vc._version)
+    with torch.no_grad():
+        flash_attn2_rs.flash_attn_with_kvcache(q, kc, vc, k=q, v=q, cache_seqlens=1)
+    assert kc._version > versions[0] and vc._version > versions[1]
+    with pytest.raises(RuntimeError, match="modified by an inplace operation"):
+        loss.backward()
+
+
+@pytest.mark.parametrize("D", [7, 20])
+def test_unpadded_head_size(D):
+    """Head sizes that are not a multiple of 8 run on padded copies; the appended
+    rows land in the caller's caches (flash_attn_interface.py:1562-1642)."""
+    B, cap, Hk, H = 2, 64, 1, 2
+    q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 2, 2, torch.float16, seed=15)
+    lengths = [3, 40]
+    got = _run(q, kc, vc, k, v, lengths, causal=True)
+    _check(got, _expect(q, kc, vc, k, v, lengths, causal=True, dtype=torch.float16))
+
+
+def test_decode_step_in_cuda_graph():
+    """A decode step (append + split attention + merge) captured in a CUDA graph
+    and replayed several times, with eager work in between, matches the eager
+    call each time."""
+    import flash_attn2_rs
+
+    B, cap, Hk, H, D = 4, 2048, 2, 8, 128
+    q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 1, 1, torch.bfloat16, seed=16)
+    q, kc, vc, k, v = (t.cuda() for t in (q, kc, vc, k, v))
+    lengths = torch.tensor([100, 900, 1500, 2000], dtype=torch.int32, device="cuda")
+
+    def step():
+        return flash_attn2_rs.flash_attn_with_kvcache(q, kc, vc, k, v, cache_seqlens=lengths, causal=True,
+                                                      num_splits=4, return_softmax_lse=True)
+
+    eager_out, eager_lse = (t.clone() for t in step())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_out, g_lse = step()
+    for i in range(3):
+        torch.randn(1000, device="cuda").sum().item()  # eager work between replays
+        g_out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, eager_out), f"replay {i}"
+        assert torch.equal(g_lse, eager_lse), f"replay {i}"
