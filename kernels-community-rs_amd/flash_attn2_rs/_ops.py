@@ -293,6 +293,24 @@ def _auto_splits(blocks, key_tiles, device):
     return int(max(1, min(128, (2 * cus + blocks - 1) // blocks, key_tiles // 4)))
 
 
+def check_cache_append(q, kcache, k, v, seqlens_k, capacity):
+    """flash_attn_interface.py:600-631: the append arguments, checked before
+    anything is written."""
+    if k is None:
+        return
+    b, sq = q.shape[0], q.shape[1]
+    if seqlens_k is None:
+        raise RuntimeError("cache lengths are required when appending K/V")
+    for name, t in (("k", k), ("v", v)):
+        if (not isinstance(t, torch.Tensor) or t.ndim != 4 or t.shape[0] != b
+                or t.shape[2:] != kcache.shape[2:] or t.dtype != q.dtype or t.device != q.device
+                or t.stride(-1) != 1):
+            raise RuntimeError(
+                f"{name} must match query batch and cache heads/dtype/device with unit last stride")
+    if k.shape != v.shape or k.shape[1] > capacity or sq > capacity:
+        raise RuntimeError("new K/V shapes must match and fit the cache capacity")
+
+
 def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=None, rotary_sin=None,
                 cache_batch_idx=None, leftpad_k=None, block_table=None, alibi_slopes=None, out=None,
                 softmax_scale=None, is_causal=False, window_size_left=-1, window_size_right=-1,
@@ -337,18 +355,7 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
         raise RuntimeError("rotary sin is required when rotary cos is supplied")
     if rotary_cos is not None and k is None:
         raise RuntimeError("rotary tables require new K/V")
-    if k is not None:
-        # flash_attn_interface.py:600-631: checked before anything is written.
-        if seqlens_k is None:
-            raise RuntimeError("cache lengths are required when appending K/V")
-        for name, t in (("k", k), ("v", v)):
-            if (not isinstance(t, torch.Tensor) or t.ndim != 4 or t.shape[0] != b
-                    or t.shape[2:] != kcache.shape[2:] or t.dtype != q.dtype or t.device != q.device
-                    or t.stride(-1) != 1):
-                raise RuntimeError(
-                    f"{name} must match query batch and cache heads/dtype/device with unit last stride")
-        if k.shape != v.shape or k.shape[1] > capacity or sq > capacity:
-            raise RuntimeError("new K/V shapes must match and fit the cache capacity")
+    check_cache_append(q, kcache, k, v, seqlens_k, capacity)
     new_keys = 0 if k is None else k.shape[1]
     if d % 8:
         # Head sizes that are not a multiple of 8 run on zero-padded copies; the

@@ -10,7 +10,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._ops import ops
+from ._ops import check_cache_append, ops
 from ._ops import torch_add_op_namespace_prefix as add_op_namespace_prefix
 from .flash_attn_interface import bwd, fwd, varlen_bwd, varlen_fwd
 
@@ -217,3 +217,79 @@ class _VarlenAttention(torch.autograd.Function):
         else:
             grads = (dq, dk, dv)
         return (*grads, *(None,) * 14)
+
+
+# flash_attn_with_kvcache as custom ops (_torch_interface.py:696-758): the
+# appending form declares the caches mutated, the read-only form mutates nothing,
+# so torch.compile / functionalization see the in-place cache writes.
+def _cached_impl(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin, cache_batch_idx,
+                 cache_leftpad, block_table, alibi_slopes, softmax_scale, causal, left, right, softcap,
+                 rotary_interleaved, num_splits):
+    out, lse = ops.fwd_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin,
+                               cache_batch_idx, cache_leftpad, block_table, alibi_slopes, None, softmax_scale,
+                               causal, left, right, softcap, rotary_interleaved, num_splits)
+    return out.contiguous(), lse
+
+
+def _cached_fake(q, *args):
+    b, sq, h, _ = q.shape
+    return torch.empty_like(q, memory_format=torch.contiguous_format), q.new_empty((b, h, sq), dtype=torch.float32)
+
+
+@torch.library.custom_op(add_op_namespace_prefix("_cached_forward"), mutates_args=("k_cache", "v_cache"),
+                         device_types="cuda")
+def _cached_forward(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k: Optional[torch.Tensor],
+                    v: Optional[torch.Tensor], cache_seqlens: Optional[torch.Tensor],
+                    rotary_cos: Optional[torch.Tensor], rotary_sin: Optional[torch.Tensor],
+                    cache_batch_idx: Optional[torch.Tensor], cache_leftpad: Optional[torch.Tensor],
+                    block_table: Optional[torch.Tensor], alibi_slopes: Optional[torch.Tensor],
+                    softmax_scale: Optional[float], causal: bool, left: int, right: int, softcap: float,
+                    rotary_interleaved: bool, num_splits: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _cached_impl(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin, cache_batch_idx,
+                        cache_leftpad, block_table, alibi_slopes, softmax_scale, causal, left, right, softcap,
+                        rotary_interleaved, num_splits)
+
+
+@torch.library.custom_op(add_op_namespace_prefix("_cached_forward_readonly"), mutates_args=(),
+                         device_types="cuda")
+def _cached_forward_readonly(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                             k: Optional[torch.Tensor], v: Optional[torch.Tensor],
+                             cache_seqlens: Optional[torch.Tensor], rotary_cos: Optional[torch.Tensor],
+                             rotary_sin: Optional[torch.Tensor], cache_batch_idx: Optional[torch.Tensor],
+                             cache_leftpad: Optional[torch.Tensor], block_table: Optional[torch.Tensor],
+                             alibi_slopes: Optional[torch.Tensor], softmax_scale: Optional[float], causal: bool,
+                             left: int, right: int, softcap: float, rotary_interleaved: bool,
+                             num_splits: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _cached_impl(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin, cache_batch_idx,
+                        cache_leftpad, block_table, alibi_slopes, softmax_scale, causal, left, right, softcap,
+                        rotary_interleaved, num_splits)
+
+
+_cached_forward.register_fake(_cached_fake)
+_cached_forward_readonly.register_fake(_cached_fake)
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
+                            cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None, block_table=None,
+                            softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                            rotary_interleaved=True, alibi_slopes=None, num_splits=0, return_softmax_lse=False):
+    if k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1:
+        raise AssertionError("k_cache / v_cache must have contiguous last dimension")
+    q, k, v = (x.contiguous() if x is not None and x.stride(-1) != 1 else x for x in (q, k, v))
+    cache_batch_idx, block_table = (x.contiguous() if x is not None and x.stride(-1) != 1 else x
+                                    for x in (cache_batch_idx, block_table))
+    if isinstance(cache_seqlens, int):
+        cache_seqlens = torch.full((q.shape[0],), cache_seqlens, device=q.device, dtype=torch.int32)
+    if k is not None and v is None:
+        raise RuntimeError("new V is required when new K is supplied")
+    capacity = k_cache.shape[1] * (block_table.shape[1] if block_table is not None else 1)
+    # Rejected appends must leave the caches (and their versions) untouched, so
+    # the checks run before the mutating op is entered.
+    check_cache_append(q, k_cache, k, v, cache_seqlens, capacity)
+    forward = _cached_forward if k is not None and (k.ndim != 4 or k.shape[1] > 0) else _cached_forward_readonly
+    out, lse = forward(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin, cache_batch_idx,
+                       cache_leftpad, block_table, alibi_slopes,
+                       None if softmax_scale is None else float(softmax_scale), bool(causal),
+                       int(window_size[0]), int(window_size[1]), float(softcap), bool(rotary_interleaved),
+                       int(num_splits))
+    return (out, lse) if return_softmax_lse else out

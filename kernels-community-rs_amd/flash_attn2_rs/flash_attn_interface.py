@@ -334,15 +334,10 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
                             rotary_interleaved=True, alibi_slopes=None, num_splits=0,
                             return_softmax_lse=False):
     """Cached inference, optionally appending K/V in place; no backward
-    (flash_attn_interface.py:1921-1960, _torch_interface.py:696-758).
-    num_splits = 0 picks the key split count for the grid."""
-    if k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1:
-        raise AssertionError("k_cache / v_cache must have contiguous last dimension")
-    q, k, v = (x.contiguous() if x is not None and x.stride(-1) != 1 else x for x in (q, k, v))
-    if isinstance(cache_seqlens, int):
-        cache_seqlens = torch.full((q.shape[0],), cache_seqlens, device=q.device, dtype=torch.int32)
-    out, lse = ops.fwd_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin,
-                               cache_batch_idx, cache_leftpad, block_table, alibi_slopes, None,
-                               softmax_scale, causal, window_size[0], window_size[1], softcap,
-                               rotary_interleaved, num_splits)
-    return (out, lse) if return_softmax_lse else out
+    (flash_attn_interface.py:1921-1960). Runs as a torch custom op
+    (_torch_interface.py:696-758); num_splits = 0 picks the key split count."""
+    from ._torch_interface import flash_attn_with_kvcache as implementation
+
+    return implementation(q, k_cache, v_cache, k, v, rotary_cos, rotary_sin, cache_seqlens, cache_batch_idx,
+                          cache_leftpad, block_table, softmax_scale, causal, window_size, softcap,
+                          rotary_interleaved, alibi_slopes, num_splits, return_softmax_lse)

@@ -291,3 +291,18 @@ def test_decode_step_in_cuda_graph():
         torch.cuda.synchronize()
         assert torch.equal(g_out, eager_out), f"replay {i}"
         assert torch.equal(g_lse, eager_lse), f"replay {i}"
+
+
+def test_cached_forward_opcheck():
+    """torch.library.opcheck of the custom ops behind flash_attn_with_kvcache
+    (schema, fake tensors, declared cache mutation)."""
+    import flash_attn2_rs  # noqa: F401
+
+    B, cap, Hk, H, D = 2, 256, 1, 2, 64
+    q, kc, vc, k, v = (t.cuda() if t is not None else None
+                       for t in _setup(B, cap, Hk, H, D, 1, 1, torch.bfloat16, seed=17))
+    lengths = torch.tensor([10, 100], dtype=torch.int32, device="cuda")
+    rest = (None, None, None, None, None, None, None, True, -1, -1, 0.0, True, 1)
+    ns = torch.ops.kcr_flash_attn2
+    torch.library.opcheck(ns._cached_forward, (q, kc, vc, k, v, lengths, *rest))
+    torch.library.opcheck(ns._cached_forward_readonly, (q, kc, vc, None, None, lengths, *rest))
