@@ -543,5 +543,36 @@ __device__ __forceinline__ uint32_t keep_bits_key_lane(const DropoutState& d, ui
     return bits;
 }
 
+// keep_bits_key_lane for a wave whose lane l holds key k with k % 32 == l % 32
+// (all 64 lanes active). The 8 Philox calls per lane above cover only 32
+// distinct counters per half-wave: (m, rb) x (k % 8) / 2. Lane 8j + 2c + e of a
+// half computes the instance (m = j, rb = e, c) once, and four exchange rounds
+// of two ds_bpermute each deliver word (k % 32) / 8 of every instance a lane
+// needs: in round s a lane publishes word (j + s) % 4 and reads the instances
+// with m = (j - s) % 4. Same bits as keep_bits_key_lane.
+__device__ __forceinline__ uint32_t keep_bits_key_lane_shared(const DropoutState& d, uint32_t bh, uint32_t q0,
+                                                              uint32_t k, int hh) {
+    const uint32_t l32 = k % 32u;
+    const uint32_t j = l32 / 8u, c = (l32 % 8u) / 2u, e = l32 & 1u;
+    uint32_t x[4];
+    philox4x32_7(d.seed, d.offset + 32ull * bh + 4u * (4u * hh + j) + c, q0 / 16u + e, k / 32u, x);
+    const uint32_t kshift = 8u * e;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const uint32_t wi = (j + s) & 3u;
+        const uint32_t pub = wi == 0 ? x[0] : wi == 1 ? x[1] : wi == 2 ? x[2] : x[3];
+        const uint32_t m = (j - s) & 3u;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const int src = 32 * hh + 8 * static_cast<int>(m) + 2 * static_cast<int>(c) + rb;
+            const uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(4 * src, static_cast<int>(pub)));
+            bits |= (((w >> kshift) & 255u) <= d.threshold ? 1u : 0u) << (8 * rb + m);
+            bits |= (((w >> (16u + kshift)) & 255u) <= d.threshold ? 1u : 0u) << (8 * rb + 4 + m);
+        }
+    }
+    return bits;
+}
+
 }  // namespace attn
 }  // namespace kcr

@@ -916,7 +916,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
             float pv[16], dsv[16];
             uint32_t keep_bits = 0xFFFFu;
             if constexpr (DROPOUT) {
-                keep_bits = keep_bits_key_lane(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + (t % gqa)),
+                keep_bits = keep_bits_key_lane_shared(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + (t % gqa)),
                                                static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh);
             }
 #pragma unroll
