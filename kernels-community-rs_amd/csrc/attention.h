@@ -543,6 +543,35 @@ __device__ __forceinline__ uint32_t keep_bits_key_lane(const DropoutState& d, ui
     return bits;
 }
 
+// keep_bits_query_lane for a wave whose lane l holds query q with q % 16 ==
+// l % 16 (all 64 lanes active). The two Philox instances a lane needs (counter
+// low bit t = 0, 1) are the same for lanes q and q ^ 8, which sit 8 apart in one
+// 16-lane DPP row: each lane computes instance t = (q % 16) / 8 and takes the
+// other from its partner with a row rotation by 8. Same bits as
+// keep_bits_query_lane.
+__device__ __forceinline__ uint32_t keep_bits_query_lane_shared(const DropoutState& d, uint32_t bh, uint32_t q,
+                                                                uint32_t kblock, int hh) {
+    const uint32_t own_t = (q % 16u) / 8u;
+    uint32_t own[4], other[4];
+    philox4x32_7(d.seed, d.offset + 32ull * bh + 4u * (q % 8u) + 2u * hh + own_t, q / 16u, kblock, own);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // DPP row_ror:8 (control 0x128): lane i of a 16-lane row reads lane (i + 8) % 16.
+        other[i] = static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(0, static_cast<int>(own[i]), 0x128, 0xF, 0xF, false));
+    }
+    const uint32_t rshift = own_t * 16u;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t t = static_cast<uint32_t>((r & 3) >> 1);
+        const uint32_t word = t == own_t ? own[r >> 2] : other[r >> 2];
+        const uint32_t byte = (word >> (rshift + 8u * (r & 1))) & 255u;
+        bits |= (byte <= d.threshold ? 1u : 0u) << r;
+    }
+    return bits;
+}
+
 // keep_bits_key_lane for a wave whose lane l holds key k with k % 32 == l % 32
 // (all 64 lanes active). The 8 Philox calls per lane above cover only 32
 // distinct counters per half-wave: (m, rb) x (k % 8) / 2. Lane 8j + 2c + e of a

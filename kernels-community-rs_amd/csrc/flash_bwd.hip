@@ -720,7 +720,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
             float dsv[16];
             uint32_t keep_bits = 0xFFFFu;
             if constexpr (DROPOUT) {
-                keep_bits = keep_bits_query_lane(drop, bh, static_cast<uint32_t>(my_row),
+                keep_bits = keep_bits_query_lane_shared(drop, bh, static_cast<uint32_t>(my_row),
                                                  static_cast<uint32_t>(kb / 32 + sub), hh);
             }
 #pragma unroll
