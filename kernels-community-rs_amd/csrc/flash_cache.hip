@@ -16,6 +16,8 @@
 // MI355X shape: one lane per 16-byte vector (8 columns) of a row; the rotary
 // partner vector is one more 16-byte load (the same vector when interleaved).
 // The op moves a few rows per sequence, so it is launch-bound, not HBM-bound.
+// Caches or sources with rows that are not 16-byte aligned (odd strides, views
+// into shared storage) take a one-element-per-lane kernel.
 
 #include "attention.h"
 
@@ -158,6 +160,80 @@ __global__ void __launch_bounds__(256) cache_update_kernel(const CacheUpdatePara
     }
 }
 
+// Caches or sources whose rows are not 16-byte aligned: one lane per element,
+// the same positions, skips and rotary arithmetic.
+template <typename T>
+__global__ void __launch_bounds__(256) cache_update_scalar_kernel(const CacheUpdateParams p) {
+    const int64_t kv_elems = p.kv_vectors * 8, q_elems = p.q_vectors * 8;
+    const int half = p.rotary_dim / 2;
+    auto rot = [&](const uint16_t* row, int dcol, uint32_t position) -> uint16_t {
+        if (dcol >= p.rotary_dim) return row[dcol];
+        bool first;
+        int other, freq;
+        if (p.interleaved) {
+            first = (dcol & 1) == 0;
+            other = dcol ^ 1;
+            freq = dcol / 2;
+        } else {
+            first = dcol < half;
+            other = first ? dcol + half : dcol - half;
+            freq = dcol % half;
+        }
+        const float a = elem_to_f32<T>(row[dcol]);
+        const float b = elem_to_f32<T>(row[other]);
+        const float c = elem_to_f32<T>(p.cos[static_cast<int64_t>(position) * half + freq]);
+        const float sn = elem_to_f32<T>(p.sin[static_cast<int64_t>(position) * half + freq]);
+        return f32_to_elem<T>(__fadd_rn(__fmul_rn(a, c), __fmul_rn(b, first ? -sn : sn)));
+    };
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < kv_elems + q_elems;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        if (i < kv_elems) {
+            const int dcol = static_cast<int>(i % p.d);
+            int64_t t = i / p.d;
+            const int h = static_cast<int>(t % p.hk);
+            t /= p.hk;
+            const int r = static_cast<int>(t % p.snew);
+            const int b = static_cast<int>(t / p.snew);
+            const int start = p.lengths[b];
+            const int64_t position = static_cast<int64_t>(start) + r;
+            if (start < 0 || position >= p.capacity || (p.rotary_dim > 0 && position >= p.rotary_rows)) continue;
+            int64_t cb, crow;
+            if (p.table) {
+                const int64_t col = position / p.page_size;
+                if (col >= p.table_cols) continue;
+                const int page = p.table[b * p.table_stride + col];
+                if (page < 0 || page >= p.cache_batches) continue;
+                cb = page;
+                crow = position % p.page_size;
+            } else {
+                const int idx = p.cache_idx ? p.cache_idx[b] : b;
+                if (idx < 0 || idx >= p.cache_batches) continue;
+                cb = idx;
+                crow = position;
+            }
+            const uint16_t* krow = p.k + b * p.k_b + r * p.k_s + h * p.k_h;
+            const uint16_t* vrow = p.v + b * p.v_b + r * p.v_s + h * p.v_h;
+            p.kc[cb * p.kc_b + crow * p.kc_s + h * p.kc_h + dcol] =
+                p.rotary_dim > 0 ? rot(krow, dcol, static_cast<uint32_t>(position)) : krow[dcol];
+            p.vc[cb * p.vc_b + crow * p.vc_s + h * p.vc_h + dcol] = vrow[dcol];
+        } else {
+            const int64_t j = i - kv_elems;
+            const int dcol = static_cast<int>(j % p.d);
+            int64_t t = j / p.d;
+            const int h = static_cast<int>(t % p.hq);
+            t /= p.hq;
+            const int r = static_cast<int>(t % p.sq);
+            const int b = static_cast<int>(t / p.sq);
+            const uint16_t* qrow = p.q + b * p.q_b + r * p.q_s + h * p.q_h;
+            const int start = p.lengths[b];
+            const int64_t position = static_cast<int64_t>(start) + (p.advance_q ? r : 0);
+            const bool rotate = start >= 0 && position < p.rotary_rows;
+            p.q_out[b * p.qo_b + r * p.qo_s + h * p.qo_h + dcol] =
+                rotate ? rot(qrow, dcol, static_cast<uint32_t>(position)) : qrow[dcol];
+        }
+    }
+}
+
 }  // namespace attn
 }  // namespace kcr
 
@@ -173,7 +249,6 @@ extern "C" int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kca
         for (auto [t, name] : {std::pair{q, "q"}, {kcache, "kcache"}, {vcache, "vcache"}, {k, "k"}, {v, "v"}}) {
             check_qkv(t, name, 4);
             if (t->dtype != q->dtype) throw type_error("cache update requires one FP16/BF16 dtype");
-            if (!rows_aligned16(t)) throw value_error(std::string(name) + " must have 16-byte aligned rows");
             require_device(t, name);
         }
         const int64_t B = q->shape[0], Sq = q->shape[1], H = q->shape[2], D = q->shape[3];
@@ -216,7 +291,7 @@ extern "C" int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kca
                 throw value_error(
                     "rotary dimension must be divisible by 16 and fit D; positions must cover cache capacity");
             }
-            if (!q_out || shape_of(*q_out) != shape_of(*q) || q_out->dtype != q->dtype || !rows_aligned16(q_out)) {
+            if (!q_out || shape_of(*q_out) != shape_of(*q) || q_out->dtype != q->dtype || q_out->strides[3] != 1) {
                 throw value_error("q_out must match q when rotary tables are given");
             }
             require_device(q_out, "q_out");
@@ -254,16 +329,31 @@ extern "C" int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kca
         p.rotary_rows = static_cast<int32_t>(rows);
         p.interleaved = interleaved ? 1 : 0;
         p.advance_q = advance_q ? 1 : 0;
+        // Work items in 8-column vectors (the scalar kernel walks 8 x as many).
+        if (D % 8 != 0) throw value_error("head size must be a multiple of 8 (pad the caches)");
         p.kv_vectors = B * k->shape[1] * Hk * (D / 8);
         p.q_vectors = rd > 0 ? B * Sq * H * (D / 8) : 0;
         const int64_t total = p.kv_vectors + p.q_vectors;
         if (total == 0) return;
-        const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536));
         auto s = static_cast<hipStream_t>(stream);
-        if (q->dtype == KCR_BFLOAT16) {
-            cache_update_kernel<bf16_t><<<grid, 256, 0, s>>>(p);
+        // 16-byte vectors need D % 8 == 0 and 16-byte aligned rows everywhere.
+        bool vec = D % 8 == 0;
+        for (auto* t : {q, kcache, vcache, k, v}) vec = vec && rows_aligned16(t);
+        if (rd > 0) vec = vec && rows_aligned16(q_out);
+        if (vec) {
+            const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536));
+            if (q->dtype == KCR_BFLOAT16) {
+                cache_update_kernel<bf16_t><<<grid, 256, 0, s>>>(p);
+            } else {
+                cache_update_kernel<f16_t><<<grid, 256, 0, s>>>(p);
+            }
         } else {
-            cache_update_kernel<f16_t><<<grid, 256, 0, s>>>(p);
+            const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total * 8 + 255) / 256, 65536));
+            if (q->dtype == KCR_BFLOAT16) {
+                cache_update_scalar_kernel<bf16_t><<<grid, 256, 0, s>>>(p);
+            } else {
+                cache_update_scalar_kernel<f16_t><<<grid, 256, 0, s>>>(p);
+            }
         }
         check_launch("launch cache_update");
     });

@@ -16,6 +16,7 @@ from .flash_attn_interface import (
     flash_attn_with_kvcache,
     fwd,
     fwd_explicit,
+    fwd_kvcache,
     varlen_bwd,
     varlen_fwd,
 )
@@ -28,6 +29,7 @@ __all__ = [
     "varlen_fwd",
     "varlen_bwd",
     "fwd_explicit",
+    "fwd_kvcache",
     "flash_attn_func",
     "flash_attn_qkvpacked_func",
     "flash_attn_kvpacked_func",

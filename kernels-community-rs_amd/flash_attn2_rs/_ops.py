@@ -351,7 +351,12 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
         raise RuntimeError("v must be a Tensor or None")
     if k is not None and v is None:
         raise RuntimeError("new V is required when new K is supplied")
-    if (rotary_cos is None) != (rotary_sin is None):
+    if rotary_cos is None:
+        # The reference ignores a sine table supplied without a cosine table.
+        if rotary_sin is not None and not isinstance(rotary_sin, torch.Tensor):
+            raise RuntimeError("rotary_sin must be a Tensor or None")
+        rotary_sin = None
+    elif rotary_sin is None:
         raise RuntimeError("rotary sin is required when rotary cos is supplied")
     if rotary_cos is not None and k is None:
         raise RuntimeError("rotary tables require new K/V")
@@ -407,6 +412,10 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
         if qp.stride(-1) != 1 or not _rows_aligned(qp):
             qp = qp.contiguous()
         rows, heads = sq, h
+    # The attention kernels move 16-byte row chunks: caches with unaligned rows
+    # are read through an aligned copy (host/layout.rs:46-125).
+    kc_att = kcache if _rows_aligned(kcache) else kcache.contiguous()
+    vc_att = vcache if _rows_aligned(vcache) else vcache.contiguous()
     cu_q = torch.arange(0, (b + 1) * rows, rows, dtype=torch.int32, device=q.device)
     out_p = torch.empty((b * rows, heads, d), dtype=q.dtype, device=q.device)
     lse_p = torch.empty((heads, b * rows), dtype=torch.float32, device=q.device)
@@ -416,7 +425,7 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     has_scale, sc = _scale_args(softmax_scale)
     call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (
-             qp, kcache, vcache, cu_q, used, leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
+             qp, kc_att, vc_att, cu_q, used, leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
          has_scale, sc, int(causal), ctypes.c_int64(left), ctypes.c_int64(right),
          ctypes.c_double(float(softcap)), ctypes.c_int64(rows), ctypes.c_int64(splits),
          ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), ref(describe(out_p)),
@@ -428,8 +437,16 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
         output = out_p.reshape(b, sq, h, d)
         lse = lse_p.reshape(h, b, sq).permute(1, 0, 2)
     if out is not None:
-        out.copy_(output)
-        output = out
+        if grouped and tuple(out.shape) == (b, h // hk, hk, d):
+            # The grouped decode layout [B, H / Hk, Hk, D] (flash_attn_interface.py:672-700,
+            # 1647-1651): filled in head order, returned as [B, 1, H, D].
+            out.copy_(output.reshape(b, hk, h // hk, d).transpose(1, 2))
+            output = out.transpose(1, 2).reshape(b, 1, h, d)
+        else:
+            if out.shape != q.shape:
+                raise RuntimeError("out must match Q or its grouped layout and have unit last stride")
+            out.copy_(output)
+            output = out
     return [output, lse.contiguous()]
 
 

@@ -328,6 +328,19 @@ def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqle
                                   alibi_slopes, deterministic, return_attn_probs, None, 2)
 
 
+def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=None, rotary_sin=None,
+                cache_batch_idx=None, leftpad_k=None, block_table=None, alibi_slopes=None, out=None,
+                softmax_scale=None, is_causal=False, window_size_left=-1, window_size_right=-1, softcap=0.0,
+                is_rotary_interleaved=False, num_splits=1):
+    """Native cached inference; appends K/V in place and returns [out, LSE]
+    (flash_attn_interface.py:1474-1700)."""
+    if q is None or isinstance(q, torch.Tensor) and not q.is_cuda:
+        _cpu_dispatch("fwd_kvcache")
+    return ops.fwd_kvcache(q, kcache, vcache, k, v, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
+                           leftpad_k, block_table, alibi_slopes, out, softmax_scale, is_causal,
+                           window_size_left, window_size_right, softcap, is_rotary_interleaved, num_splits)
+
+
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,
                             cache_seqlens=None, cache_batch_idx=None, cache_leftpad=None, block_table=None,
                             softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
