@@ -597,6 +597,8 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 // Two LDS stages, one barrier per tile; 2 waves per SIMD.
 // ---------------------------------------------------------------------------
 
+constexpr int kLook = 4;  // operand reads in flight ahead of their MFMA (v2 kernels)
+
 template <typename T, int D, int NW, bool VARLEN, bool DROPOUT>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {
     constexpr int BN = 64;
@@ -700,17 +702,34 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
         const uint16_t* vl = v_lds + (t & 1) * TILE;
         if (t + 1 < ntiles) copy_tile(kb + BN, (t + 1) & 1);
 
+        // S^T = K Q^T and dP^T = V dO^T: step i reads K (even i) or V (odd i) of
+        // key half (i / 2) % 2 at k-step i / 4, kLook MFMAs ahead of its use.
         f32x16 s[2], dp[2];
         s[0] = s[1] = dp[0] = dp[1] = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
-                const u32x4 ka = tl.rm(kl, sub, ks);
-                const u32x4 va = tl.rm(vl, sub, ks);
-                s[sub] = mfma32<T>(ka, qf[ks], s[sub]);
-                dp[sub] = mfma32<T>(va, dof[ks], dp[sub]);
-            }
+        {
+            constexpr int N = 4 * KS;
+            auto load = [&](auto ic) __attribute__((always_inline)) -> u32x4 {
+                constexpr int i = decltype(ic)::value;
+                return tl.rm((i & 1) ? vl : kl, (i >> 1) & 1, i >> 2);
+            };
+            u32x4 ring[kLook];
+            static_for<0, kLook>([&](auto ic) __attribute__((always_inline)) { ring[decltype(ic)::value] = load(ic); });
+            __builtin_amdgcn_sched_group_barrier(0x100, kLook, 0);
+            static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                constexpr int sub = (i >> 1) & 1, ks = i >> 2;
+                const u32x4 a = ring[i % kLook];
+                if constexpr (i + kLook < N) {
+                    ring[i % kLook] = load(std::integral_constant<int, i + kLook>{});
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                if constexpr (i & 1) {
+                    dp[sub] = mfma32<T>(a, dof[ks], dp[sub]);
+                } else {
+                    s[sub] = mfma32<T>(a, qf[ks], s[sub]);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            });
         }
         const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
                                (wl >= 0 && kb < last_row + off - wl);
@@ -740,13 +759,26 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
                 for (int w = 0; w < 4; ++w) pk[2 * sub + t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
             }
         }
-        // dQ^T += K^T dS^T (K^T read transposed from the key tile)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                acc[db] = mfma32<T>(tl.tr(kl, db, tt), pk[tt], acc[db]);
-            }
+        // dQ^T += K^T dS^T (K^T read transposed from the key tile); step i:
+        // db = i % DB, tt = i / DB, reads ahead as above.
+        {
+            constexpr int N = 4 * DB;
+            u32x4 ring[kLook];
+            static_for<0, kLook>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                ring[i] = tl.tr(kl, i % DB, i / DB);
+            });
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLook, 0);
+            static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                const u32x4 a = ring[i % kLook];
+                if constexpr (i + kLook < N) {
+                    ring[i % kLook] = tl.tr(kl, (i + kLook) % DB, (i + kLook) / DB);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+                acc[i % DB] = mfma32<T>(a, pk[i / DB], acc[i % DB]);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            });
         }
         wait_vmem();
         __syncthreads();
