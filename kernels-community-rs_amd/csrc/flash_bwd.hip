@@ -934,15 +934,35 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                                (wl >= 0 && key0 < qb + BQ - 1 + off - wl);
 #pragma unroll
         for (int qc = 0; qc < NQC; ++qc) {
+            // S = Q K^T and dP = dO V^T; the operands of k-step ks + 1 are read
+            // while the MFMAs of k-step ks run.
             f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                s = mfma32<T>(tl.rm(ql, qc, ks), kf[ks], s);
-                if constexpr (V_LDS) {
-                    dp = mfma32<T>(tl.rm(dl, qc, ks), tl.rm(v_lds, wave, ks), dp);
-                } else {
-                    dp = mfma32<T>(tl.rm(dl, qc, ks), vf[ks], dp);
-                }
+            {
+                constexpr int NR = V_LDS ? 3 : 2;
+                auto rd = [&](auto ic, u32x4 (&r)[NR]) __attribute__((always_inline)) {
+                    constexpr int ks = decltype(ic)::value;
+                    r[0] = tl.rm(ql, qc, ks);
+                    r[1] = tl.rm(dl, qc, ks);
+                    if constexpr (V_LDS) r[2] = tl.rm(v_lds, wave, ks);
+                };
+                u32x4 ra[2][NR];
+                rd(std::integral_constant<int, 0>{}, ra[0]);
+                __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+                static_for<0, KS>([&](auto ic) __attribute__((always_inline)) {
+                    constexpr int ks = decltype(ic)::value;
+                    if constexpr (ks + 1 < KS) {
+                        rd(std::integral_constant<int, ks + 1>{}, ra[(ks + 1) & 1]);
+                        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+                    }
+                    const u32x4(&r)[NR] = ra[ks & 1];
+                    s = mfma32<T>(r[0], kf[ks], s);
+                    if constexpr (V_LDS) {
+                        dp = mfma32<T>(r[1], r[2], dp);
+                    } else {
+                        dp = mfma32<T>(r[1], vf[ks], dp);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                });
             }
             u32x4 pP[2], pS[2];
             float pv[16], dsv[16];
@@ -981,15 +1001,29 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                     pS[t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
                 }
             }
-            // dV^T += dO^T P and dK^T += Q^T dS (transposed reads of the query tiles)
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-#pragma unroll
-                for (int t2 = 0; t2 < 2; ++t2) {
-                    const int tt = 2 * qc + t2;
-                    dv[db] = mfma32<T>(tl.tr(dl, db, tt), pP[t2], dv[db]);
-                    dk[db] = mfma32<T>(tl.tr(ql, db, tt), pS[t2], dk[db]);
-                }
+            // dV^T += dO^T P and dK^T += Q^T dS (transposed reads of the query
+            // tiles), step i = (db, t2) with the next step's operands in flight.
+            {
+                auto rd = [&](auto ic, u32x4 (&r)[2]) __attribute__((always_inline)) {
+                    constexpr int i = decltype(ic)::value;
+                    r[0] = tl.tr(dl, i >> 1, 2 * qc + (i & 1));
+                    r[1] = tl.tr(ql, i >> 1, 2 * qc + (i & 1));
+                };
+                u32x4 rb[2][2];
+                rd(std::integral_constant<int, 0>{}, rb[0]);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                static_for<0, 2 * DB>([&](auto ic) __attribute__((always_inline)) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int db = i >> 1, t2 = i & 1;
+                    if constexpr (i + 1 < 2 * DB) {
+                        rd(std::integral_constant<int, i + 1>{}, rb[(i + 1) & 1]);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                    }
+                    const u32x4(&r)[2] = rb[i & 1];
+                    dv[db] = mfma32<T>(r[0], pP[t2], dv[db]);
+                    dk[db] = mfma32<T>(r[1], pS[t2], dk[db]);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                });
             }
         }
         wait_vmem();
