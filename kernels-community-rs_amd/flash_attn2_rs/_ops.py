@@ -154,6 +154,13 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
             raise ValueError("dropout requires RNG state")
         if not _rng_state_ok(state, q):
             raise ValueError("RNG state must be contiguous int64 [2] on q's device")
+    batch = cu_seqlens_q.numel() - 1
+    tq, h, d = q.shape
+    hk = k.shape[1]
+    if (int(max_q) == 1 and tq == batch and h > hk and hk > 0 and h % hk == 0 and alibi is None
+            and float(np.float32(p)) == 0.0 and int(left) < 0 and int(right) < 0):
+        return _grouped_decode(q, k, v, cu_seqlens_k, seqused_k, leftpad_k, scale, softcap, max_k,
+                               zero_tensors)
     qp, kp, vp = _packed(q), _packed(k), _packed(v)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
@@ -166,6 +173,29 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
          ref(describe(out)), ref(describe(lse)), stream_of(q))
     probabilities = torch.empty(0, dtype=q.dtype, device=q.device)
     return [out, lse, probabilities]
+
+
+def _grouped_decode(q, k, v, cu_seqlens_k, seqused_k, leftpad_k, scale, softcap, max_k, zero_tensors):
+    """One query per sequence with GQA (host/varlen/mod.rs:310-372, packed_grouped):
+    the H / Hk query heads of a KV head become the query rows of one sequence, so
+    each K/V tile is read once per KV head. A single query sees every key, causal
+    or not (varlen/mod.rs:250-268). Returns [out [B, H, D], lse [H, B], probs]."""
+    b, h, d = q.shape
+    hk = k.shape[1]
+    g = h // hk
+    qg = q.reshape(b, hk, g, d).transpose(1, 2).reshape(b * g, hk, d).contiguous()
+    cu_q = torch.arange(0, (b + 1) * g, g, dtype=torch.int32, device=q.device)
+    out_g = torch.empty_like(qg)
+    lse_g = torch.empty((hk, b * g), dtype=torch.float32, device=q.device)
+    has_scale, sc = _scale_args(scale)
+    call("kcr_flash_varlen_fwd", *(ref(describe(t)) for t in (
+             qg, _packed(k), _packed(v), cu_q, cu_seqlens_k, seqused_k, leftpad_k, None)),
+         has_scale, sc, 0, ctypes.c_int64(-1), ctypes.c_int64(-1), ctypes.c_double(float(softcap)), None,
+         ctypes.c_int64(g), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)), ref(describe(out_g)),
+         ref(describe(lse_g)), stream_of(q))
+    out = out_g.reshape(b, g, hk, d).transpose(1, 2).reshape(b, h, d)
+    lse = lse_g.reshape(hk, b, g).permute(0, 2, 1).reshape(h, b)
+    return [out, lse, torch.empty(0, dtype=q.dtype, device=q.device)]
 
 
 def _paged_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi, scale, causal,

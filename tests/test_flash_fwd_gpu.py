@@ -7,6 +7,8 @@ Bars: the reference tests' tolerances (bf16: atol 1e-2, rtol 5e-2, mean 8e-3, LS
 <= 2e-2 against the fp32 softmax(QK^T)V oracle.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -166,3 +168,25 @@ def test_varlen_baseline_config():
                             v[None, a:bnd, 2:3].float().numpy(), causal=True)
         assert np.abs(out[a:bnd, 8:12].float().cpu().numpy() - eo[0]).max() <= 2e-2
         np.testing.assert_allclose(lse[8:12, a:bnd].cpu().numpy(), el[0], atol=8e-2, rtol=0)
+
+
+def test_varlen_grouped_decode_lse():
+    """test_gold.py:600-617: one query per sequence with GQA (the grouped decode
+    path); out against the oracle and LSE against a float64 logsumexp, LSE
+    contiguous [H, B]."""
+    import flash_attn2_rs
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(16, 8, 128, generator=g).half()
+    k = torch.randn(16, 1024, 2, 128, generator=g).half()
+    v = torch.randn(16, 1024, 2, 128, generator=g).half()
+    cu_q = torch.arange(17, dtype=torch.int32)
+    out, lse, _ = flash_attn2_rs.ops.varlen_fwd_explicit(
+        q.cuda(), k.flatten(0, 1).cuda(), v.flatten(0, 1).cuda(), cu_q.cuda(), (cu_q * 1024).cuda(), None,
+        None, None, None, True, -1, -1, 0.0, 0.0, None, 1, 1024, False, False)
+    eo, _ = OA.varlen_forward(q.float().numpy(), k.flatten(0, 1).float().numpy(), v.flatten(0, 1).float().numpy(),
+                              cu_q.numpy(), (cu_q * 1024).numpy(), causal=True)
+    assert np.abs(out.float().cpu().numpy() - eo).max() <= 2e-2
+    scores = torch.einsum("bhd,bkhd->bhk", q.double(), k.double().repeat_interleave(4, 2)) / math.sqrt(128)
+    np.testing.assert_allclose(lse.cpu().numpy(), scores.logsumexp(-1).T.numpy(), atol=5e-3, rtol=0)
+    assert lse.is_contiguous() and lse.shape == (8, 16)
