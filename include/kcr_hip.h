@@ -185,7 +185,11 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
  *   rows [leftpad_k[b], seqused_k[b]) (seqused_k = cache lengths after the append)
  *   of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
  *   (int32 [B, max_blocks]; head size 64 or 128, no softcap/ALiBi). out like q;
- *   lse float32 [H, Tq]. Windows are normalised against the cache capacity.
+ *   lse float32 [H, Tq]. Batched form: cu_seqlens_q NULL, q and out [B, R, H, D]
+ *   with any 16-byte aligned row strides (e.g. the grouped decode view of
+ *   [B, 1, H*G, D] as [B, G, H, D]) and lse float32 [B, H, R] with unit last
+ *   stride; max_seqlen_q is taken as R. Windows are normalised against the cache
+ *   capacity.
  *   num_splits > 1 splits each query tile's keys over that many blocks; the fp32
  *   partials go to `workspace` (kcr_flash_fwd_kvcache_workspace_bytes bytes,
  *   16-byte aligned) and a merge kernel writes out/lse. Softcap / ALiBi / other

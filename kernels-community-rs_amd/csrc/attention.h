@@ -132,6 +132,11 @@ struct FwdParams {
     int32_t n_splits;
     float* o_part;
     float* lse_part;
+    // Batched cache queries: rows_per_seq > 0 means q/o [B, rows_per_seq, H, D]
+    // and lse [B, H, rows_per_seq] addressed through q_b / o_b / lse_b, with no
+    // cu_q; sequence b's rows are packed rows b * rows_per_seq .. for the
+    // split partials. 0: packed rows through cu_q (q_b = o_b = lse_b = 0).
+    int32_t rows_per_seq;
 };
 
 // Packed-sequence bounds of sequence b (device/varlen/mod.rs:79-136): query rows
@@ -146,8 +151,8 @@ struct VarSeq {
 
 __device__ __forceinline__ VarSeq varlen_seq(const FwdParams& p, int b) {
     VarSeq r{};
-    const int qs = p.cu_q[b];
-    const int qe = p.cu_q[b + 1];
+    const int qs = p.rows_per_seq ? b * p.rows_per_seq : p.cu_q[b];
+    const int qe = p.rows_per_seq ? qs + p.rows_per_seq : p.cu_q[b + 1];
     int ks = 0, ke = p.capacity;
     int64_t kbatch = 0;
     if (p.cache_mode) {

@@ -104,16 +104,18 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     int64_t q_off = 0, k_off = 0;
     int sq = p.seqlen_q, sk = p.seqlen_k;
     int lse_row0 = 0;
+    [[maybe_unused]] int part_row0 = 0;  // row of the split partials (packed row index)
     int64_t k_batch = 0;
     if constexpr (VARLEN) {
         const VarSeq vs = varlen_seq(p, b);
         if (!vs.ok) return;
         sq = vs.sq;
         sk = vs.sk;
-        q_off = static_cast<int64_t>(vs.qs);
+        q_off = p.rows_per_seq ? 0 : static_cast<int64_t>(vs.qs);
         k_off = vs.k_row0;
         k_batch = vs.k_batch;
-        lse_row0 = vs.qs;
+        lse_row0 = static_cast<int>(q_off);
+        part_row0 = vs.qs;
         qb = (sq + BM - 1) / BM - 1 - qo;
         if (qb < 0) return;
     }
@@ -128,17 +130,17 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
     const uint16_t* vbase;
     uint16_t* obase;
     if constexpr (VARLEN) {
-        qbase = static_cast<const uint16_t*>(p.q) + q_off * p.q_s + head * p.q_h;
+        qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + q_off * p.q_s + head * p.q_h;
         kbase = static_cast<const uint16_t*>(p.k) + k_batch * p.k_b + k_off * p.k_s + kvh * p.k_h;
         vbase = static_cast<const uint16_t*>(p.v) + k_batch * p.v_b + k_off * p.v_s + kvh * p.v_h;
-        obase = static_cast<uint16_t*>(p.o) + q_off * p.o_s + head * p.o_h;
+        obase = static_cast<uint16_t*>(p.o) + b * p.o_b + q_off * p.o_s + head * p.o_h;
     } else {
         qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
         kbase = static_cast<const uint16_t*>(p.k) + b * p.k_b + kvh * p.k_h;
         vbase = static_cast<const uint16_t*>(p.v) + b * p.v_b + kvh * p.v_h;
         obase = static_cast<uint16_t*>(p.o) + b * p.o_b + head * p.o_h;
     }
-    float* lse_base = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + lse_row0;
+    float* lse_base = p.lse + b * p.lse_b + head * p.lse_h + lse_row0;
 
     // ---- key range of this query tile (device/config.rs:183-207) ----
     const int last_row = min(row0 + BM, sq) - 1;
@@ -513,16 +515,18 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     int64_t q_off = 0, k_off = 0;
     int sq = p.seqlen_q, sk = p.seqlen_k;
     int lse_row0 = 0;
+    int part_row0 = 0;  // row of the split partials (packed row index)
     int64_t k_batch = 0;
     if constexpr (VARLEN) {
         const VarSeq vs = varlen_seq(p, b);
         if (!vs.ok) return;
         sq = vs.sq;
         sk = vs.sk;
-        q_off = static_cast<int64_t>(vs.qs);
+        q_off = p.rows_per_seq ? 0 : static_cast<int64_t>(vs.qs);
         k_off = vs.k_row0;
         k_batch = vs.k_batch;
-        lse_row0 = vs.qs;
+        lse_row0 = static_cast<int>(q_off);
+        part_row0 = vs.qs;
         qb = (sq + BM - 1) / BM - 1 - qo;
         if (qb < 0) return;
     }
@@ -537,17 +541,17 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     const uint16_t* vbase;
     uint16_t* obase;
     if constexpr (VARLEN) {
-        qbase = static_cast<const uint16_t*>(p.q) + q_off * p.q_s + head * p.q_h;
+        qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + q_off * p.q_s + head * p.q_h;
         kbase = static_cast<const uint16_t*>(p.k) + k_batch * p.k_b + k_off * p.k_s + kvh * p.k_h;
         vbase = static_cast<const uint16_t*>(p.v) + k_batch * p.v_b + k_off * p.v_s + kvh * p.v_h;
-        obase = static_cast<uint16_t*>(p.o) + q_off * p.o_s + head * p.o_h;
+        obase = static_cast<uint16_t*>(p.o) + b * p.o_b + q_off * p.o_s + head * p.o_h;
     } else {
         qbase = static_cast<const uint16_t*>(p.q) + b * p.q_b + head * p.q_h;
         kbase = static_cast<const uint16_t*>(p.k) + b * p.k_b + kvh * p.k_h;
         vbase = static_cast<const uint16_t*>(p.v) + b * p.v_b + kvh * p.v_h;
         obase = static_cast<uint16_t*>(p.o) + b * p.o_b + head * p.o_h;
     }
-    float* lse_base = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + lse_row0;
+    float* lse_base = p.lse + b * p.lse_b + head * p.lse_h + lse_row0;
 
     const int last_row = min(row0 + BM, sq) - 1;
     int kv_end = sk;
@@ -718,7 +722,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         // -inf when the split saw no key of the row.
         if (row < sq) {
             const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-            const int64_t prow = (static_cast<int64_t>(split) * p.heads + head) * p.total_q + lse_row0 + row;
+            const int64_t prow = (static_cast<int64_t>(split) * p.heads + head) * p.total_q + part_row0 + row;
             float* op = p.o_part + prow * D;
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
@@ -1065,12 +1069,15 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
 // Split-KV merge (flash-attn2-rs/src/device/varlen/merge.rs): per row,
 // LSE = log sum_i exp(LSE_i) and O = sum_i exp(LSE_i - LSE) O_i over the splits;
 // a row no split saw gets O = 0 and LSE = +inf, as an empty row does. One wave
-// per (head, packed row); lane l < D / 2 owns columns 2l and 2l + 1.
+// per (head, packed row); lane l < D / 2 owns columns 2l and 2l + 1. Packed row
+// t is row t % rows_per_seq of sequence t / rows_per_seq in out / lse
+// (rows_per_seq = total_q with zero batch strides for packed outputs).
 template <typename T, int D>
 __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restrict__ o_part,
                                                            const float* __restrict__ lse_part, int n_splits,
-                                                           int heads, int total_q, uint16_t* __restrict__ o,
-                                                           int64_t o_s, int64_t o_h, float* __restrict__ lse,
+                                                           int heads, int total_q, int rows_per_seq,
+                                                           uint16_t* __restrict__ o, int64_t o_b, int64_t o_s,
+                                                           int64_t o_h, float* __restrict__ lse, int64_t lse_b,
                                                            int64_t lse_h) {
     static_assert(D % 2 == 0 && D <= 128, "two columns per lane");
     constexpr int PER = 2;
@@ -1098,11 +1105,14 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restri
             }
         }
     }
+    const int seq = row / rows_per_seq;
+    const int r = row - seq * rows_per_seq;
     if (lane < D / 2) {
-        uint16_t* dst = o + static_cast<int64_t>(row) * o_s + static_cast<int64_t>(head) * o_h + PER * lane;
+        uint16_t* dst =
+            o + seq * o_b + static_cast<int64_t>(r) * o_s + static_cast<int64_t>(head) * o_h + PER * lane;
         *reinterpret_cast<uint32_t*>(dst) = pack2<T>(acc[0], acc[1]);
     }
-    if (lane == 0) lse[static_cast<int64_t>(head) * lse_h + row] = out_lse;
+    if (lane == 0) lse[seq * lse_b + static_cast<int64_t>(head) * lse_h + r] = out_lse;
 }
 
 // Empty-key rows: O = 0, LSE = +inf (host/forward/mod.rs:548-572). Also clears
@@ -1518,18 +1528,26 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
                                      int64_t workspace_bytes, const kcr_tensor* out, const kcr_tensor* lse,
                                      void* stream) {
     return guarded([&] {
-        check_qkv(q, "q", 3);
+        // Batched form: q/out [B, R, H, D] (any strides) and lse [B, H, R], no cu_seqlens_q.
+        const bool batched = q && q->ndim == 4 && !cu_seqlens_q;
+        check_qkv(q, "q", batched ? 4 : 3);
         check_qkv(kcache, "kcache", 4);
         check_qkv(vcache, "vcache", 4);
         if (kcache->dtype != q->dtype || vcache->dtype != q->dtype) {
             throw type_error("q, kcache and vcache must share dtype (all f16 or all bf16)");
         }
         if (shape_of(*kcache) != shape_of(*vcache)) throw value_error("K/V cache shapes must match");
-        if (!cu_seqlens_q || cu_seqlens_q->ndim != 1 || cu_seqlens_q->shape[0] < 2) {
+        if (!batched && (!cu_seqlens_q || cu_seqlens_q->ndim != 1 || cu_seqlens_q->shape[0] < 2)) {
             throw value_error("cu_seqlens_q must have shape [batch + 1]");
         }
-        const int64_t batch = cu_seqlens_q->shape[0] - 1;
-        const int64_t Tq = q->shape[0], H = q->shape[1], D = q->shape[2];
+        const int64_t batch = batched ? q->shape[0] : cu_seqlens_q->shape[0] - 1;
+        const int64_t R = batched ? q->shape[1] : 0;
+        if (batched) {
+            if (R <= 0 || R > 65535) throw value_error("batched q needs 1..65535 rows per sequence");
+            max_seqlen_q = R;
+        }
+        const int64_t Tq = batched ? batch * R : q->shape[0];
+        const int64_t H = q->shape[batched ? 2 : 1], D = q->shape[batched ? 3 : 2];
         const int64_t Bc = kcache->shape[0], S = kcache->shape[1], Hk = kcache->shape[2];
         check_head_dim(D);
         if (kcache->shape[3] != D) throw value_error("K/V cache shapes must match Q's head size");
@@ -1547,7 +1565,7 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
             require_device(t, name);
         };
         if (!seqused_k) throw value_error("seqused_k (cache lengths after the append) is required");
-        check_meta(cu_seqlens_q, {batch + 1}, "cu_seqlens_q");
+        if (!batched) check_meta(cu_seqlens_q, {batch + 1}, "cu_seqlens_q");
         check_meta(seqused_k, {batch}, "seqused_k");
         check_meta(leftpad_k, {batch}, "leftpad_k");
         check_meta(cache_batch_idx, {batch}, "cache_batch_idx");
@@ -1566,11 +1584,16 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
         if (capacity > INT32_MAX - 256 || Bc * S > INT32_MAX) throw value_error("cache/query dimensions must fit int32");
         int32_t alibi_b = 0;
         check_alibi(alibi, batch, H, alibi_b);
-        if (!out || shape_of(*out) != shape_of(*q) || out->dtype != q->dtype || out->strides[2] != 1) {
+        if (!out || shape_of(*out) != shape_of(*q) || out->dtype != q->dtype || out->strides[out->ndim - 1] != 1) {
             throw value_error("out must match q's shape and dtype with unit last stride");
         }
-        if (!lse || lse->dtype != KCR_FLOAT32 || lse->ndim != 2 || lse->shape[0] != H || lse->shape[1] != Tq ||
-            !is_contiguous(*lse)) {
+        if (batched) {
+            if (!lse || lse->dtype != KCR_FLOAT32 || shape_of(*lse) != std::vector<int64_t>{batch, H, R} ||
+                lse->strides[2] != 1) {
+                throw value_error("lse must be float32 [batch, H, rows] with unit last stride");
+            }
+        } else if (!lse || lse->dtype != KCR_FLOAT32 || lse->ndim != 2 || lse->shape[0] != H ||
+                   lse->shape[1] != Tq || !is_contiguous(*lse)) {
             throw value_error("lse must be contiguous float32 [H, total_q]");
         }
         for (auto* t : {q, kcache, vcache, out}) {
@@ -1592,16 +1615,25 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
         prm.o = out->data;
         prm.lse = static_cast<float*>(lse->data);
         prm.alibi = alibi ? static_cast<const float*>(alibi->data) : nullptr;
-        prm.cu_q = static_cast<const int32_t*>(cu_seqlens_q->data);
         prm.seqused_k = static_cast<const int32_t*>(seqused_k->data);
         prm.leftpad_k = leftpad_k ? static_cast<const int32_t*>(leftpad_k->data) : nullptr;
         prm.total_q = static_cast<int32_t>(Tq);
-        prm.q_s = q->strides[0]; prm.q_h = q->strides[1];
         prm.k_b = kcache->strides[0]; prm.k_s = kcache->strides[1]; prm.k_h = kcache->strides[2];
         prm.v_b = vcache->strides[0]; prm.v_s = vcache->strides[1]; prm.v_h = vcache->strides[2];
-        prm.o_s = out->strides[0]; prm.o_h = out->strides[1];
-        prm.lse_b = 0;
-        prm.lse_h = Tq;
+        if (batched) {
+            prm.rows_per_seq = static_cast<int32_t>(R);
+            prm.q_b = q->strides[0]; prm.q_s = q->strides[1]; prm.q_h = q->strides[2];
+            prm.o_b = out->strides[0]; prm.o_s = out->strides[1]; prm.o_h = out->strides[2];
+            prm.lse_b = lse->strides[0];
+            prm.lse_h = lse->strides[1];
+        } else {
+            prm.cu_q = static_cast<const int32_t*>(cu_seqlens_q->data);
+            prm.q_s = q->strides[0]; prm.q_h = q->strides[1];
+            prm.o_s = out->strides[0]; prm.o_h = out->strides[1];
+            prm.lse_b = 0;
+            prm.lse_h = Tq;
+        }
+        const int rows = batched ? static_cast<int>(R) : static_cast<int>(Tq);
         prm.batch = static_cast<int32_t>(batch);
         prm.heads = static_cast<int32_t>(H);
         prm.kv_heads = static_cast<int32_t>(Hk);
@@ -1657,15 +1689,13 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
             auto merge = [&](auto tag) {
                 using T = decltype(tag);
                 if (bucket == 64) {
-                    merge_splits_kernel<T, 64><<<grid, 256, 0, s>>>(prm.o_part, prm.lse_part, prm.n_splits,
-                                                                    prm.heads, prm.total_q,
-                                                                    static_cast<uint16_t*>(prm.o), prm.o_s,
-                                                                    prm.o_h, prm.lse, prm.lse_h);
+                    merge_splits_kernel<T, 64><<<grid, 256, 0, s>>>(
+                        prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
+                        static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
                 } else {
-                    merge_splits_kernel<T, 128><<<grid, 256, 0, s>>>(prm.o_part, prm.lse_part, prm.n_splits,
-                                                                     prm.heads, prm.total_q,
-                                                                     static_cast<uint16_t*>(prm.o), prm.o_s,
-                                                                     prm.o_h, prm.lse, prm.lse_h);
+                    merge_splits_kernel<T, 128><<<grid, 256, 0, s>>>(
+                        prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
+                        static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
                 }
             };
             if (q->dtype == KCR_BFLOAT16) {

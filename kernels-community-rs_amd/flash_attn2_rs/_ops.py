@@ -432,52 +432,60 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
     else:
         used = (seqlens_k.to(torch.int32) + new_keys).contiguous()
     grouped = sq == 1 and h > hk and left < 0 and right < 0 and alibi_slopes is None
+    # The kernels take q / out as [B, rows, heads, D] views and lse as [B, heads, rows]
+    # through their strides, so the caller's tensors are used in place.
+    if out is not None and out.shape != q.shape and not (grouped and tuple(out.shape) == (b, h // hk, hk, d)):
+        raise RuntimeError("out must match Q or its grouped layout and have unit last stride")
+    if out is not None and out.stride(-1) != 1:
+        raise RuntimeError("out must match Q or its grouped layout and have unit last stride")
+    output = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
     if grouped:
+        # Query heads hk * G .. hk * G + G - 1 become the G query rows of KV head hk
+        # (host/varlen/mod.rs:310-372); one query row sees every key either way.
         g = h // hk
-        qp = q.reshape(b, hk, g, d).transpose(1, 2).reshape(b * g, hk, d).contiguous()
         rows, heads = g, hk
-        causal = False  # one query row sees every key either way
+        causal = False
+        qp = q.reshape(b, hk, g, d).transpose(1, 2)
+        if tuple(output.shape) == (b, g, hk, d):
+            # The grouped decode layout [B, H / Hk, Hk, D] (flash_attn_interface.py:672-700,
+            # 1647-1651) is already [B, rows, heads, D].
+            op = output
+        else:
+            op = output.view(b, hk, g, d).transpose(1, 2) if output.is_contiguous() else None
+        lse_p = lse.view(b, hk, g)
     else:
-        qp = q.reshape(b * sq, h, d)
-        if qp.stride(-1) != 1 or not _rows_aligned(qp):
-            qp = qp.contiguous()
         rows, heads = sq, h
+        qp, op, lse_p = q, output, lse
+    if not _rows_aligned(qp):
+        qp = qp.contiguous()
     # The attention kernels move 16-byte row chunks: caches with unaligned rows
     # are read through an aligned copy (host/layout.rs:46-125).
     kc_att = kcache if _rows_aligned(kcache) else kcache.contiguous()
     vc_att = vcache if _rows_aligned(vcache) else vcache.contiguous()
-    cu_q = torch.arange(0, (b + 1) * rows, rows, dtype=torch.int32, device=q.device)
-    out_p = torch.empty((b * rows, heads, d), dtype=q.dtype, device=q.device)
-    lse_p = torch.empty((heads, b * rows), dtype=torch.float32, device=q.device)
+    tmp = op is None or not _rows_aligned(op)
+    if tmp:
+        op = torch.empty((b, rows, heads, d), dtype=q.dtype, device=q.device)
     if splits < 1:
         splits = _auto_splits(b * heads * ((rows + 127) // 128), (capacity + 63) // 64, q.device)
     ws_bytes = lib.kcr_flash_fwd_kvcache_workspace_bytes(splits, heads, b * rows, d)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     has_scale, sc = _scale_args(softmax_scale)
     call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (
-             qp, kc_att, vc_att, cu_q, used, leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
+             qp, kc_att, vc_att, None, used, leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
          has_scale, sc, int(causal), ctypes.c_int64(left), ctypes.c_int64(right),
          ctypes.c_double(float(softcap)), ctypes.c_int64(rows), ctypes.c_int64(splits),
-         ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), ref(describe(out_p)),
+         ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), ref(describe(op)),
          ref(describe(lse_p)), stream_of(q))
-    if grouped:
-        output = out_p.reshape(b, g, hk, d).transpose(1, 2).reshape(b, 1, h, d)
-        lse = lse_p.reshape(hk, b, g).permute(1, 0, 2).reshape(b, h, 1)
-    else:
-        output = out_p.reshape(b, sq, h, d)
-        lse = lse_p.reshape(h, b, sq).permute(1, 0, 2)
-    if out is not None:
-        if grouped and tuple(out.shape) == (b, h // hk, hk, d):
-            # The grouped decode layout [B, H / Hk, Hk, D] (flash_attn_interface.py:672-700,
-            # 1647-1651): filled in head order, returned as [B, 1, H, D].
-            out.copy_(output.reshape(b, hk, h // hk, d).transpose(1, 2))
-            output = out.transpose(1, 2).reshape(b, 1, h, d)
+    if tmp:
+        if tuple(output.shape) == tuple(op.shape):
+            output.copy_(op)
         else:
-            if out.shape != q.shape:
-                raise RuntimeError("out must match Q or its grouped layout and have unit last stride")
-            out.copy_(output)
-            output = out
-    return [output, lse.contiguous()]
+            output.copy_(op.transpose(1, 2).reshape(b, 1, h, d))
+    if tuple(output.shape) != (b, sq, h, d):
+        # Grouped layout out: returned in head order as [B, 1, H, D].
+        output = output.transpose(1, 2).reshape(b, 1, h, d)
+    return [output, lse]
 
 
 ops = SimpleNamespace(
