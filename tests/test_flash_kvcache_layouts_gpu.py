@@ -233,3 +233,33 @@ def test_grouped_decode_layout():
     # Query head h = kvh * 4 + j sits at grouped[:, j, kvh].
     np.testing.assert_allclose(_np(grouped).transpose(0, 2, 1, 3).reshape(2, 8, 128), eo[:, 0],
                                atol=7e-3 + 0.04 * np.abs(eo).max())
+
+
+@pytest.mark.parametrize("grouped", [True, False])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_out_views_written_in_place(grouped, splits):
+    """`out` as a strided view (padded rows: written in place) and with unaligned
+    rows (written through a temporary) gives the same bits as a fresh output,
+    and the caller's tensor holds the result."""
+    import flash_attn2_rs
+
+    torch.manual_seed(3)
+    B, Hk, D = 3, 2, 128
+    H, sq = (8, 1) if grouped else (4, 3)
+    q = torch.randn(B, sq, H, D + 8, device="cuda", dtype=torch.bfloat16)[..., :D]
+    kc = torch.randn(B, 768, Hk, D, device="cuda", dtype=q.dtype)
+    vc = torch.randn_like(kc)
+    lengths = torch.tensor([5, 300, 767], dtype=torch.int32, device="cuda")
+    ref_out, ref_lse = flash_attn2_rs.fwd_kvcache(q, kc, vc, seqlens_k=lengths, is_causal=True,
+                                                  num_splits=splits)
+    eo, el, _, _ = _expected(q, kc, vc, None, None, lengths.cpu().numpy(), causal=True, dtype="bf16")
+    _close(ref_out, ref_lse, eo, el)
+    for pad in (8, 4):
+        backing = torch.full((B, sq, H, D + pad), 7.0, device="cuda", dtype=q.dtype)
+        view = backing[..., :D]
+        out, lse = flash_attn2_rs.fwd_kvcache(q, kc, vc, seqlens_k=lengths, is_causal=True,
+                                              num_splits=splits, out=view)
+        torch.cuda.synchronize()
+        assert torch.equal(view, ref_out) and torch.equal(out, ref_out)
+        assert torch.equal(lse, ref_lse)
+        assert bool((backing[..., D:] == 7.0).all())  # padding columns untouched
