@@ -356,11 +356,22 @@ __device__ __forceinline__ void static_for(F&& f) {
 // buffer `rsrc` (descriptor words) at `voffset` into LDS at `lds_base` + 16 * lane.
 // The compiler does not see these copies, so it inserts no wait for them before
 // later LDS reads; the caller orders them with explicit vmcnt waits and barriers.
+// NT sets the non-temporal cache policy, for data that no other block reads
+// again (measured on MI355X: a decode K/V stream runs at ~6.8 TB/s with it and
+// ~5.5 TB/s without).
+template <bool NT = false>
 __device__ __forceinline__ void dma_lds16(const u32x4& rsrc, uint32_t lds_base, uint32_t voffset) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :
-                 : "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_base)))
-                 : "memory", "m0");
+    if constexpr (NT) {
+        asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                     :
+                     : "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_base)))
+                     : "memory", "m0");
+    } else {
+        asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                     :
+                     : "v"(voffset), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(lds_base)))
+                     : "memory", "m0");
+    }
 }
 
 // Same with 4 bytes per lane (LDS at `lds_base` + 4 * lane).
@@ -389,8 +400,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
 // elements) into a swizzled tile by direct HBM -> LDS loads; rows at or past
 // `rows_valid` read as zero (buffer range check). The NW waves move 1 KB blocks
-// of 8 (D = 64) or 4 (D = 128) rows.
-template <int D, int NW, int ROWS>
+// of 8 (D = 64) or 4 (D = 128) rows. NT: non-temporal copies (see dma_lds16).
+template <int D, int NW, int ROWS, bool NT = false>
 __device__ __forceinline__ void copy_rows_dma(const uint16_t* base, int64_t row_stride, int rows_valid,
                                               uint16_t* tile, int wave, int lane) {
     constexpr int CH = D / 8;
@@ -408,7 +419,7 @@ __device__ __forceinline__ void copy_rows_dma(const uint16_t* base, int64_t row_
     for (int i = 0; i < IPW; ++i) {
         const int blk = wave * IPW + i;
         const int gc = (lane % CH) ^ kv_swizzle<CH>(blk * RPB + rr);
-        dma_lds16(r, tile_lds + blk * 1024u, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u);
+        dma_lds16<NT>(r, tile_lds + blk * 1024u, static_cast<uint32_t>(blk * RPB + rr) * row_bytes + gc * 16u);
     }
 }
 

@@ -448,9 +448,11 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // ds_read_b128 and V^T, the A operand of O^T = V^T P^T, with ds_read_b64_tr_b16
 // from the same row-major tile. P^T stays in registers: the fp32 scores are
 // packed in place into the B operand of the PV MFMA. Two LDS stages, the next
-// tile's copy in flight during the current tile, one barrier per tile.
+// tile's copy in flight during the current tile, one barrier per tile. STREAM:
+// every K/V tile is read by this block only (cache decode with grouped rows),
+// so the copies are non-temporal.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool VARLEN, bool DROPOUT>
+template <typename T, int D, bool VARLEN, bool DROPOUT, bool STREAM>
 __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams p) {
     constexpr int NW = 4;
     constexpr int BN = kBN;
@@ -586,8 +588,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
                 if (page < 0) rows = 0;
             }
         }
-        copy_rows_dma<D, NW, BN>(kt, p.k_s, rows, k_lds + stage * TILE, wave, lane);
-        copy_rows_dma<D, NW, BN>(vt, p.v_s, rows, v_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, BN, STREAM>(kt, p.k_s, rows, k_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, BN, STREAM>(vt, p.v_s, rows, v_lds + stage * TILE, wave, lane);
     };
 
     int ntiles = kv_begin < kv_end ? (kv_end - kv_begin + BN - 1) / BN : 0;
@@ -1195,9 +1197,17 @@ void launch_tiled(FwdParams& prm, hipStream_t s) {
     // equal work); masked dense grids keep the longest-first tile-major order.
     prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
     if (prm.drop_threshold < 255) {
-        flash_fwd_tiled_kernel<T, D, VARLEN, true><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+        flash_fwd_tiled_kernel<T, D, VARLEN, true, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+    } else if constexpr (VARLEN) {
+        if (prm.cache_mode && prm.q_blocks == 1 && prm.heads == prm.kv_heads) {
+            // One query tile per sequence and one query head per KV head (e.g.
+            // grouped decode rows): each K/V tile is read by one block only.
+            flash_fwd_tiled_kernel<T, D, true, false, true><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+        } else {
+            flash_fwd_tiled_kernel<T, D, true, false, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+        }
     } else {
-        flash_fwd_tiled_kernel<T, D, VARLEN, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+        flash_fwd_tiled_kernel<T, D, false, false, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
     }
     check_launch("launch flash_fwd");
 }
