@@ -182,8 +182,8 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
  * flash-attn2-rs/src/host/varlen/mod.rs:36-670, device/varlen/mod.rs:60-170,
  * device/varlen/paged.rs, device/varlen/merge.rs).
  *   q [Tq, H, D] packed with cu_seqlens_q int32 [B+1]; sequence b attends to cache
- *   rows [leftpad_k[b], seqused_k[b]) (seqused_k = cache lengths after the append)
- *   of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
+ *   rows [leftpad_k[b], seqused_k[b] + new_keys) (seqused_k: cache lengths before
+ *   an append of new_keys rows; NULL: every row of the cache) of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
  *   (int32 [B, max_blocks]; head size 64 or 128, no softcap/ALiBi). out like q;
  *   lse float32 [H, Tq]. Batched form: cu_seqlens_q NULL, q and out [B, R, H, D]
  *   with any 16-byte aligned row strides (e.g. the grouped decode view of
@@ -197,7 +197,7 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
 int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int64_t heads, int64_t total_q,
                                               int64_t head_dim);
 int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
-                          const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k,
+                          const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k, int64_t new_keys,
                           const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
                           const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
                           double scale, int causal, int64_t window_left, int64_t window_right,

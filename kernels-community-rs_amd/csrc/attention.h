@@ -137,6 +137,8 @@ struct FwdParams {
     // cu_q; sequence b's rows are packed rows b * rows_per_seq .. for the
     // split partials. 0: packed rows through cu_q (q_b = o_b = lse_b = 0).
     int32_t rows_per_seq;
+    // Added to every seqused_k entry (cache mode: the appended rows).
+    int32_t seqused_add;
 };
 
 // Packed-sequence bounds of sequence b (device/varlen/mod.rs:79-136): query rows
@@ -164,7 +166,7 @@ __device__ __forceinline__ VarSeq varlen_seq(const FwdParams& p, int b) {
         ks = p.cu_k[b];
         ke = p.cu_k[b + 1];
     }
-    const int len = p.seqused_k ? p.seqused_k[b] : ke - ks;
+    const int len = p.seqused_k ? p.seqused_k[b] + p.seqused_add : ke - ks;
     const int pad = p.leftpad_k ? p.leftpad_k[b] : 0;
     if (qs < 0 || qe < qs || qe > p.total_q || ks < 0 || ke < ks || (!p.cache_mode && ke > p.total_k) ||
         pad < 0 || len < pad || len > ke - ks || qe - qs > p.seqlen_q) {

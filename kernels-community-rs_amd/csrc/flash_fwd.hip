@@ -521,7 +521,18 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     int64_t k_batch = 0;
     if constexpr (VARLEN) {
         const VarSeq vs = varlen_seq(p, b);
-        if (!vs.ok) return;
+        if (!vs.ok) {
+            // Batched split partials have no fill: mark this block's rows as
+            // unseen (LSE -inf) so the merge gives O = 0, LSE = +inf.
+            if (nsplit > 1 && p.rows_per_seq > 0) {
+                const int r = (p.q_blocks - 1 - qo) * BM + wave * 32 + l32;
+                if (hh == 0 && r < p.rows_per_seq) {
+                    p.lse_part[(static_cast<int64_t>(split) * p.heads + head) * p.total_q +
+                               static_cast<int64_t>(b) * p.rows_per_seq + r] = -INFINITY;
+                }
+            }
+            return;
+        }
         sq = vs.sq;
         sk = vs.sk;
         q_off = p.rows_per_seq ? 0 : static_cast<int64_t>(vs.qs);
@@ -1531,7 +1542,7 @@ extern "C" int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int
 
 extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
                                      const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k,
-                                     const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                                     int64_t new_keys, const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
                                      const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
                                      double scale, int causal, int64_t window_left, int64_t window_right,
                                      double softcap, int64_t max_seqlen_q, int64_t num_splits, void* workspace,
@@ -1574,7 +1585,7 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
             }
             require_device(t, name);
         };
-        if (!seqused_k) throw value_error("seqused_k (cache lengths after the append) is required");
+        if (new_keys < 0 || new_keys > INT32_MAX) throw value_error("new_keys must be in 0..=i32::MAX");
         if (!batched) check_meta(cu_seqlens_q, {batch + 1}, "cu_seqlens_q");
         check_meta(seqused_k, {batch}, "seqused_k");
         check_meta(leftpad_k, {batch}, "leftpad_k");
@@ -1625,7 +1636,8 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
         prm.o = out->data;
         prm.lse = static_cast<float*>(lse->data);
         prm.alibi = alibi ? static_cast<const float*>(alibi->data) : nullptr;
-        prm.seqused_k = static_cast<const int32_t*>(seqused_k->data);
+        prm.seqused_k = seqused_k ? static_cast<const int32_t*>(seqused_k->data) : nullptr;
+        prm.seqused_add = static_cast<int32_t>(new_keys);
         prm.leftpad_k = leftpad_k ? static_cast<const int32_t*>(leftpad_k->data) : nullptr;
         prm.total_q = static_cast<int32_t>(Tq);
         prm.k_b = kcache->strides[0]; prm.k_s = kcache->strides[1]; prm.k_h = kcache->strides[2];
@@ -1689,8 +1701,9 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
             prm.n_splits = static_cast<int32_t>(splits);
             prm.o_part = static_cast<float*>(workspace);
             prm.lse_part = prm.o_part + splits * H * Tq * bucket;
-            // Splits that see no row of an invalid sequence leave LSE -inf.
-            fill_f32(prm.lse_part, splits * H * Tq, -INFINITY, s);
+            // Packed rows of an invalid sequence are unknown to its blocks: start
+            // every partial LSE at -inf (batched blocks write their own).
+            if (!batched) fill_f32(prm.lse_part, splits * H * Tq, -INFINITY, s);
         }
         launch_fwd<true>(prm, q->dtype, bucket, general, s);
         if (splits > 1) {

@@ -214,8 +214,8 @@ def _paged_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k,
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
     has_scale, sc = _scale_args(scale)
-    call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (
-             qp, k, v, cu_seqlens_q, seqused_k, None, None, block_table, alibi)),
+    call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (qp, k, v, cu_seqlens_q, seqused_k)),
+         ctypes.c_int64(0), *(ref(describe(t)) for t in (None, None, block_table, alibi)),
          has_scale, sc, int(bool(causal)), ctypes.c_int64(int(left)), ctypes.c_int64(int(right)),
          ctypes.c_double(float(softcap)), ctypes.c_int64(int(max_q)), ctypes.c_int64(1),
          ctypes.c_void_p(0), ctypes.c_int64(0), ref(describe(out)), ref(describe(lse)), stream_of(q))
@@ -426,11 +426,9 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
             # Native writes bypass torch's in-place ops: bump the versions so
             # autograd sees the caches changed.
             torch.autograd.graph.increment_version((kcache, vcache))
-    # Cache rows attended: [leftpad, seqlens_k + new) (all rows without lengths).
-    if seqlens_k is None:
-        used = torch.full((b,), capacity, dtype=torch.int32, device=q.device)
-    else:
-        used = (seqlens_k.to(torch.int32) + new_keys).contiguous()
+    # Cache rows attended: [leftpad, seqlens_k + new) (all rows without lengths);
+    # the kernels add new_keys to the lengths.
+    used = None if seqlens_k is None else seqlens_k.to(torch.int32).contiguous()
     grouped = sq == 1 and h > hk and left < 0 and right < 0 and alibi_slopes is None
     # The kernels take q / out as [B, rows, heads, D] views and lse as [B, heads, rows]
     # through their strides, so the caller's tensors are used in place.
@@ -471,8 +469,9 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
     ws_bytes = lib.kcr_flash_fwd_kvcache_workspace_bytes(splits, heads, b * rows, d)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     has_scale, sc = _scale_args(softmax_scale)
-    call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (
-             qp, kc_att, vc_att, None, used, leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
+    call("kcr_flash_fwd_kvcache", *(ref(describe(t)) for t in (qp, kc_att, vc_att, None, used)),
+         ctypes.c_int64(0 if used is None else new_keys),
+         *(ref(describe(t)) for t in (leftpad_k, cache_batch_idx, block_table, alibi_slopes)),
          has_scale, sc, int(causal), ctypes.c_int64(left), ctypes.c_int64(right),
          ctypes.c_double(float(softcap)), ctypes.c_int64(rows), ctypes.c_int64(splits),
          ctypes.c_void_p(ws.data_ptr()), ctypes.c_int64(ws.numel()), ref(describe(op)),

@@ -178,6 +178,21 @@ def test_empty_cache_row_and_out_of_range_positions():
     assert torch.count_nonzero(out) == 0 and torch.isinf(lse).all() and (lse > 0).all()
 
 
+@pytest.mark.parametrize("H", [8, 2])
+def test_split_invalid_sequence_is_empty(H):
+    """Key splits with a sequence whose cache batch index is out of range: its
+    blocks write nothing but "unseen" partials, so the merge gives O = 0 and
+    LSE = +inf for it; the other sequence is unaffected."""
+    B, cap, Hk, D = 2, 1024, 2, 128
+    q, kc, vc, _, _ = _setup(B, cap, Hk, H, D, 0, 1, torch.bfloat16, seed=13)
+    lengths = [700, 300]
+    out, lse, _, _ = _run(q, kc, vc, None, None, lengths, idx=[1, 7], splits=3)
+    eo, el, _, _ = _expect(q[:1], kc, vc, None, None, lengths[:1], idx=[1])
+    _check((out[:1], lse[:1], kc, vc), (eo, el, kc.float().numpy(), vc.float().numpy()))
+    assert torch.count_nonzero(out[1]) == 0
+    assert torch.isinf(lse[1]).all() and (lse[1] > 0).all()
+
+
 def test_split_merge_matches_unsplit():
     """Key splits (explicit counts) reproduce the unsplit result within fp32 merge
     rounding."""
