@@ -161,8 +161,9 @@ __global__ void __launch_bounds__(256) bwd_preprocess_kernel(
             c = out + b * o_b + s * o_s + h * o_h;
         }
         for (int d = lane * 8; d < head_dim; d += lanes_per_row * 8) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(a + d);
-            const u32x4 y = *reinterpret_cast<const u32x4*>(c + d);
+            // dO and O are read once: non-temporal loads.
+            const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a + d));
+            const u32x4 y = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(c + d));
             float fx[8], fy[8];
             unpack8<T>(x, fx);
             unpack8<T>(y, fy);
