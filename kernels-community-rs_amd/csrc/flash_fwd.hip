@@ -622,6 +622,15 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         const uint16_t* kl = k_lds + (t & 1) * TILE;
         const uint16_t* vl = v_lds + (t & 1) * TILE;
         if (t + 1 < ntiles) copy_tile(kb + BN, (t + 1) & 1);
+        if constexpr (STREAM) {
+            // Waves whose rows all lie past the sequence (3 of 4 with 4 grouped
+            // decode rows) only share the copies and the barrier.
+            if (row0 + wave * 32 >= sq) {
+                wait_vmem();
+                __syncthreads();
+                continue;
+            }
+        }
 
         // S^T = K Q^T for the 64 keys of the tile (two 32-key halves); the K
         // reads run kLookTiled MFMAs ahead of their use.
