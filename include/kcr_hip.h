@@ -183,7 +183,8 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
  * device/varlen/paged.rs, device/varlen/merge.rs).
  *   q [Tq, H, D] packed with cu_seqlens_q int32 [B+1]; sequence b attends to cache
  *   rows [leftpad_k[b], seqused_k[b] + new_keys) (seqused_k: cache lengths before
- *   an append of new_keys rows; NULL: every row of the cache) of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
+ *   an append of new_keys rows; NULL: every row of the cache, new_keys ignored)
+ *   of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
  *   (int32 [B, max_blocks]; head size 64 or 128, no softcap/ALiBi). out like q;
  *   lse float32 [H, Tq]. Batched form: cu_seqlens_q NULL, q and out [B, R, H, D]
  *   with any 16-byte aligned row strides (e.g. the grouped decode view of
