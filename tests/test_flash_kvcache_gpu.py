@@ -108,6 +108,17 @@ def test_chunked_prefill_causal(splits, D):
     _check(got, _expect(q, kc, vc, k, v, lengths, causal=True))
 
 
+@pytest.mark.parametrize("splits", [1, 3])
+def test_long_chunk_two_query_tiles(splits):
+    """A 200-token chunk (two 128-row query tiles per sequence) appended and
+    attended causally, with and without key splits."""
+    B, cap, Hk, H, D = 2, 1024, 2, 4, 128
+    q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 200, 200, torch.bfloat16, seed=14)
+    lengths = [0, 300]
+    got = _run(q, kc, vc, k, v, lengths, causal=True, splits=splits)
+    _check(got, _expect(q, kc, vc, k, v, lengths, causal=True))
+
+
 @pytest.mark.parametrize("splits", [1, 2])
 @pytest.mark.parametrize("D", [64, 128])
 def test_paged_cache(splits, D):
