@@ -195,9 +195,10 @@ def _wl_fa_varlen(kind):
 
 def wl_fa_kvcache_decode():
     """flash_attn_with_kvcache decode step (an inference path with no benchmark
-    config of its own): B=16 sequences with 8191 cached tokens each, one new token appended, Hq=32,
-    Hkv=8, D=128 bf16, causal, automatic key splits. HBM-bound: the step reads the
-    whole K/V cache once, 16 x 8192 x 8 x 128 x 2 x 2 = 536,870,912 B."""
+    config of its own): B=16 sequences with 8191 cached tokens each, one new
+    token appended, Hq=32, Hkv=8, D=128 bf16, causal, automatic key splits.
+    HBM-bound: the step reads the whole K/V cache once,
+    16 x 8192 x 8 x 128 x 2 x 2 = 536,870,912 B."""
     import flash_attn2_rs
 
     b, hq, hkv, d, cap = 16, 32, 8, 128, 8192
