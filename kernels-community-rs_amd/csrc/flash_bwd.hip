@@ -598,7 +598,7 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 // Two LDS stages, one barrier per tile; 2 waves per SIMD.
 // ---------------------------------------------------------------------------
 
-constexpr int kLook = 4;  // operand reads in flight ahead of their MFMA (v2 kernels)
+constexpr int kLook = 3;  // operand reads in flight ahead of their MFMA (v2 kernels)
 
 template <typename T, int D, int NW, bool VARLEN, bool DROPOUT>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {

@@ -46,8 +46,8 @@ __device__ __forceinline__ int vt_swizzle(int row) {
     const int x = (row >> 4) & 7;
     return (x & 1) | ((x & 6) << 1);
 }
-constexpr float kRescaleSlack = 8.0f;
-constexpr int kLookTiled = 4;  // operand reads in flight ahead of their MFMA (tiled kernel)  // log2 units the running max may lag behind
+constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag behind
+constexpr int kLookTiled = 3;          // operand reads in flight ahead of their MFMA (tiled kernel)
 
 // GENERAL covers softcap, ALiBi and head sizes below the compiled bucket (zeroed
 // lanes of the padded head dimension); the fast path is the plain scaled dot

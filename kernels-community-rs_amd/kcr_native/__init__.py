@@ -98,26 +98,22 @@ def _load():
 lib = _load()
 
 
+_DIMS = ctypes.c_int64 * KCR_MAX_DIMS
+
+
 def describe(t):
-    """A `kcr_tensor` for a torch tensor (or a null pointer for None)."""
+    """A `kcr_tensor` for a torch tensor (or a null pointer for None). Built in
+    one constructor call: it runs for every tensor of every op call."""
     if t is None:
         return None
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"expected a Tensor, got {type(t).__name__}")
-    if t.ndim > KCR_MAX_DIMS:
-        raise ValueError(f"tensors of rank {t.ndim} are not supported (at most {KCR_MAX_DIMS})")
-    d = KcrTensor()
-    d.data = t.data_ptr() if t.numel() > 0 or t.data_ptr() else 0
-    d.dtype = DTYPE_CODES.get(t.dtype, DTYPE_OTHER)
-    d.ndim = t.ndim
-    d.device = t.device.index if t.device.type == "cuda" and t.device.index is not None else (
-        0 if t.device.type == "cuda" else -1
-    )
-    d.reserved = 0
-    for i, (n, s) in enumerate(zip(t.shape, t.stride())):
-        d.shape[i] = n
-        d.strides[i] = s
-    return d
+    nd = t.dim()
+    if nd > KCR_MAX_DIMS:
+        raise ValueError(f"tensors of rank {nd} are not supported (at most {KCR_MAX_DIMS})")
+    # get_device(): the CUDA device index, -1 for host tensors.
+    return KcrTensor(t.data_ptr(), DTYPE_CODES.get(t.dtype, DTYPE_OTHER), nd, t.get_device(), 0,
+                     _DIMS(*t.shape), _DIMS(*t.stride()))
 
 
 def ref(desc):
