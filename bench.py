@@ -69,6 +69,49 @@ def wl_rmsnorm():
                 cpu=lambda: cpu_rmsnorm(x, w))
 
 
+def wl_rmsnorm_bwd():
+    """RMSNorm backward at the forward's shape: dx and the per-block fp32 weight
+    gradient partials, then their fixed-order reduction into dw."""
+    import rmsnorm
+
+    g = _gen(3)
+    rows, n = 16384, 4096
+    x = torch.randn(rows, n, generator=g).bfloat16().cuda()
+    dy = torch.randn(rows, n, generator=g).bfloat16().cuda()
+    w = (torch.rand(n, generator=g) + 0.5).bfloat16().cuda()
+    rstd = torch.empty(rows, device="cuda")
+    rmsnorm.ops.rms_norm_forward(torch.empty_like(x), rstd, x, w, 1e-6, 0.0, "llama")
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    blocks = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    dw_partial = torch.empty(blocks, n, dtype=torch.float32, device="cuda")
+
+    def run():
+        rmsnorm.ops.rms_norm_backward(dx, dw_partial, dy, x, w, rstd, 0.0, "llama")
+        rmsnorm.ops.rms_norm_reduce_weight_grad(dw, dw_partial)
+
+    # Algorithmic: read x, dy, w, rstd; write dx, dw (the partials are overhead).
+    bytes_ = rows * n * 2 * 3 + n * 2 * 2 + rows * 4
+    return dict(run=run, work=bytes_, bound="hbm", kernel="rms_bwd_block",
+                config={"x": [rows, n], "dtype": "bf16", "casting_mode": "llama"}, cpu=None)
+
+
+def wl_silu():
+    """Elementwise silu (one of the non-gated activations) on the gated
+    workload's output shape."""
+    import activation_rs
+
+    g = _gen(4)
+    x = torch.randn(16384, 14336, generator=g).bfloat16().cuda()
+    out = torch.empty_like(x)
+
+    def run():
+        activation_rs.ops.silu(out, x)
+
+    return dict(run=run, work=2 * x.numel() * 2, bound="hbm", kernel="activation_vec",
+                config={"x": list(x.shape), "dtype": "bf16"}, cpu=None)
+
+
 def _wl_gated(op):
     def make():
         import activation_rs
@@ -244,9 +287,11 @@ WORKLOADS = {
     "fa_varlen_fwd": _wl_fa_varlen("fwd"),
     "fa_varlen_bwd": _wl_fa_varlen("bwd"),
     "rms_norm": wl_rmsnorm,
+    "rms_norm_bwd": wl_rmsnorm_bwd,
     "silu_and_mul": _wl_gated("silu_and_mul"),
     "gelu_and_mul": _wl_gated("gelu_and_mul"),
     "gelu_tanh_and_mul": _wl_gated("gelu_tanh_and_mul"),
+    "silu": wl_silu,
     "fa_kvcache_decode": wl_fa_kvcache_decode,
     "hbm_copy": wl_hbm_copy,
 }

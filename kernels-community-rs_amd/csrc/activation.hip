@@ -271,23 +271,35 @@ __global__ void __launch_bounds__(kThreads) activation_vec(u32x4* __restrict__ o
                                                            const u32x4* __restrict__ in,
                                                            uint64_t total) {
     constexpr int VEC = vec_elems<T>();
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
-         i += stride * kUnroll) {
-        u32x4 xs[kUnroll];
+    // Same memory shape as act_and_mul_vec: kGatedUnroll consecutive 256-vector
+    // chunks per block and iteration over a capped, grid-strided grid.
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads * kGatedUnroll;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads * kGatedUnroll + threadIdx.x; i < total;
+         i += stride) {
+        u32x4 xs[kGatedUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint64_t j = i + u * stride;
+        for (int u = 0; u < kGatedUnroll; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * kThreads;
             if (j < total) xs[u] = __builtin_nontemporal_load(in + j);
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint64_t j = i + u * stride;
+        for (int u = 0; u < kGatedUnroll; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * kThreads;
             if (j >= total) continue;
             float x[VEC], r[VEC];
             widen<T>(xs[u], x);
+            // The fast activation forms of the gated kernel, under the same
+            // per-vector coverage check.
+            bool fast = has_fast_form<T, A>();
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) r[e] = apply_act<T, A>(x[e], 0.0f);
+            for (int e = 0; e < VEC; ++e) fast = fast && fast_form_covers<A>(x[e]);
+            if (fast) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) r[e] = apply_act<T, A, true>(x[e], 0.0f);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) r[e] = apply_act<T, A>(x[e], 0.0f);
+            }
             __builtin_nontemporal_store(narrow<T>(r), out + j);
         }
     }
@@ -422,7 +434,9 @@ void launch_elementwise_t(const kcr_tensor* out, const kcr_tensor* input, const 
     const uint64_t total_elems = static_cast<uint64_t>(l.tokens) * static_cast<uint64_t>(l.d);
     if (total_elems % VEC == 0 && aligned16(out->data) && aligned16(input->data)) {
         const uint64_t total = total_elems / VEC;
-        activation_vec<T, A><<<grid_for(total), kThreads, 0, stream>>>(
+        const uint64_t need = (total + kThreads * kGatedUnroll - 1) / (kThreads * kGatedUnroll);
+        const unsigned grid = static_cast<unsigned>(std::max<uint64_t>(1, std::min(need, kGatedBlocks)));
+        activation_vec<T, A><<<grid, kThreads, 0, stream>>>(
             static_cast<u32x4*>(out->data), static_cast<const u32x4*>(input->data), total);
     } else {
         activation_scalar<T, A><<<grid_for(total_elems), kThreads, 0, stream>>>(

@@ -261,15 +261,42 @@ __global__ void __launch_bounds__(1024) rms_bwd_block(X* dx, float* __restrict__
 }
 
 // dw[c] = sum_b dw_partial[b, c] in a fixed order, rounded to W (device.rs:339-358).
+// One block per 64 columns (a lane per column). Each of the 16 waves sums a
+// contiguous run of partial rows in order, with 8 loads in flight; wave 0 then
+// adds the 16 run sums in order. The order is fixed, so results repeat bit for
+// bit (it differs from one sequential chain only by fp32 rounding).
+constexpr int kReduceWaves = 16;
 template <typename W>
-__global__ void __launch_bounds__(256) reduce_weight_grad(W* __restrict__ dw,
-                                                          const float* __restrict__ dw_partial,
-                                                          uint32_t blocks, uint32_t n) {
-    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= n) return;
+__global__ void __launch_bounds__(64 * kReduceWaves) reduce_weight_grad(W* __restrict__ dw,
+                                                                        const float* __restrict__ dw_partial,
+                                                                        uint32_t blocks, uint32_t n) {
+    __shared__ float run_sum[kReduceWaves][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.x * 64 + lane;
+    const uint32_t per = (blocks + kReduceWaves - 1) / kReduceWaves;
+    const uint32_t b0 = min(static_cast<uint32_t>(wave) * per, blocks);
+    const uint32_t b1 = min(b0 + per, blocks);
     float sum = 0.0f;
-    for (uint32_t b = 0; b < blocks; ++b) sum += dw_partial[static_cast<uint64_t>(b) * n + c];
-    Elem<W>::store(dw + c, sum);
+    if (c < n) {
+        uint32_t b = b0;
+        for (; b + 8 <= b1; b += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = dw_partial[static_cast<uint64_t>(b + u) * n + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sum += v[u];
+        }
+        for (; b < b1; ++b) sum += dw_partial[static_cast<uint64_t>(b) * n + c];
+    }
+    run_sum[wave][lane] = sum;
+    __syncthreads();
+    if (wave == 0 && c < n) {
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kReduceWaves; ++w) total += run_sum[w][lane];
+        Elem<W>::store(dw + c, total);
+    }
 }
 
 namespace {
@@ -543,19 +570,20 @@ extern "C" int kcr_rms_norm_reduce_weight_grad(const kcr_tensor* dw, const kcr_t
         check_contiguous(dw, "dw");
         check_contiguous(dw_partial, "dw_partial");
         auto s = static_cast<hipStream_t>(stream);
-        const unsigned grid = static_cast<unsigned>((n + 255) / 256);
+        const unsigned grid = static_cast<unsigned>((n + 63) / 64);
+        constexpr unsigned threads = 64 * kReduceWaves;
         const auto* p = static_cast<const float*>(dw_partial->data);
         switch (dw->dtype) {
             case KCR_FLOAT16:
-                reduce_weight_grad<f16_t><<<grid, 256, 0, s>>>(static_cast<f16_t*>(dw->data), p,
+                reduce_weight_grad<f16_t><<<grid, threads, 0, s>>>(static_cast<f16_t*>(dw->data), p,
                                                                blocks, n);
                 break;
             case KCR_BFLOAT16:
-                reduce_weight_grad<bf16_t><<<grid, 256, 0, s>>>(static_cast<bf16_t*>(dw->data), p,
+                reduce_weight_grad<bf16_t><<<grid, threads, 0, s>>>(static_cast<bf16_t*>(dw->data), p,
                                                                 blocks, n);
                 break;
             case KCR_FLOAT32:
-                reduce_weight_grad<float><<<grid, 256, 0, s>>>(static_cast<float*>(dw->data), p,
+                reduce_weight_grad<float><<<grid, threads, 0, s>>>(static_cast<float*>(dw->data), p,
                                                                blocks, n);
                 break;
             default:
