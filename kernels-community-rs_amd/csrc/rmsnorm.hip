@@ -17,6 +17,8 @@
 // `reduce_weight_grad` in a fixed order.
 #include "common.h"
 
+#include <type_traits>
+
 namespace kcr {
 
 enum Mode : int { MODE_LLAMA = 0, MODE_GEMMA = 1, MODE_NONE = 2 };
@@ -260,6 +262,103 @@ __global__ void __launch_bounds__(1024) rms_bwd_block(X* dx, float* __restrict__
     }
 }
 
+// Backward with one wave per partial-gradient row: the wave owns rows
+// [part * per, (part + 1) * per), reads each row's dy and x once with 16-byte
+// loads (CHUNKS vectors per lane), and keeps the row's fp32 dw contributions in
+// registers, summed over its rows in order. Same arithmetic and rounding points
+// as rms_bwd_block. Requires W == X (16-bit), n % 8 == 0 and 16-byte aligned
+// tensors. dy may alias dx (each row is read whole before it is written).
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
+__global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __restrict__ dw_partial,
+                                                           const u32x4* dy, const u32x4* __restrict__ x,
+                                                           const u32x4* __restrict__ weight,
+                                                           const float* __restrict__ rstd, uint32_t rows,
+                                                           uint32_t nvec, uint32_t parts, float inv_n,
+                                                           float offset) {
+    constexpr int VEC = vec_of<X>();
+    static_assert(VEC == 8, "16-bit element types");
+    const int lane = threadIdx.x & 63;
+    const uint32_t part = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (part >= parts) return;
+    const uint32_t per = (rows + parts - 1) / parts;
+    const uint64_t r0 = static_cast<uint64_t>(part) * per;
+    const uint64_t r1 = r0 + per < rows ? r0 + per : rows;
+
+    u32x4 wv[CHUNKS];
+    if constexpr (AFFINE) {
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) wv[c] = weight[v];
+        }
+    }
+    float acc[AFFINE ? CHUNKS * VEC : 1];
+#pragma unroll
+    for (int i = 0; i < (AFFINE ? CHUNKS * VEC : 1); ++i) acc[i] = 0.0f;
+
+    for (uint64_t row = r0; row < r1; ++row) {
+        const uint64_t base = row * nvec;
+        u32x4 gv[CHUNKS], xv[CHUNKS];
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) {
+                gv[c] = dy[base + v];
+                xv[c] = __builtin_nontemporal_load(x + base + v);
+            }
+        }
+        const float r = rstd[row];
+        float dot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) {
+                float g[VEC], xf[VEC], wf[VEC];
+                widen16<X>(gv[c], g);
+                widen16<X>(xv[c], xf);
+                if constexpr (AFFINE) widen16<W>(wv[c], wf);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) dot += (AFFINE ? g[e] * (wf[e] + offset) : g[e]) * xf[e];
+            }
+        }
+        dot = wave_sum(dot);
+        const float correction = -inv_n * r * r * dot;
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) {
+                float g[VEC], xf[VEC], wf[VEC], o[VEC];
+                widen16<X>(gv[c], g);
+                widen16<X>(xv[c], xf);
+                if constexpr (AFFINE) widen16<W>(wv[c], wf);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const float gg = AFFINE ? g[e] * (wf[e] + offset) : g[e];
+                    o[e] = r * gg + r * (correction * xf[e]);
+                    if constexpr (AFFINE) {
+                        const bool rw = Casting<M>::round_weight_grad;
+                        const float x_hat = rw ? rnd<X>(xf[e] * r) : xf[e] * r;
+                        acc[c * VEC + e] += rw ? rnd<X>(g[e] * x_hat) : g[e] * x_hat;
+                    }
+                }
+                __builtin_nontemporal_store(narrow16<X>(o), dx + base + v);
+            }
+        }
+    }
+    if constexpr (AFFINE) {
+        float4* dwr = reinterpret_cast<float4*>(dw_partial + static_cast<uint64_t>(part) * nvec * VEC);
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t v = lane + 64u * c;
+            if (v < nvec) {
+                const float* a = acc + c * VEC;
+                dwr[2 * v] = float4{a[0], a[1], a[2], a[3]};
+                dwr[2 * v + 1] = float4{a[4], a[5], a[6], a[7]};
+            }
+        }
+    }
+}
+
 // dw[c] = sum_b dw_partial[b, c] in a fixed order, rounded to W (device.rs:339-358).
 // One block per 64 columns (a lane per column). Each of the 16 waves sums a
 // contiguous run of partial rows in order, with 8 loads in flight; wave 0 then
@@ -470,6 +569,31 @@ struct BwdLaunch {
         // Without dy the gradient is read from dx (in place).
         const void* dy = b.dy ? b.dy->data : b.dx->data;
         float* dwp = AFFINE ? static_cast<float*>(b.dw_partial->data) : nullptr;
+        constexpr bool kWaveForm = vec_of<X>() == 8 && (!AFFINE || std::is_same<W, X>::value);
+        if constexpr (kWaveForm) {
+            const bool aligned = aligned16(b.dx->data) && aligned16(dy) && aligned16(b.x->data) &&
+                                 (!AFFINE || (aligned16(b.w->data) && aligned16(dwp)));
+            const uint32_t nvec = static_cast<uint32_t>(b.n / 8);
+            if (aligned && b.n % 8 == 0 && nvec <= 512 && b.blocks <= 0xffffffffll) {
+                auto go = [&](auto chunks_tag) {
+                    constexpr int CH = decltype(chunks_tag)::value;
+                    const uint64_t grid = (static_cast<uint64_t>(b.blocks) + kWaves - 1) / kWaves;
+                    rms_bwd_wave<X, W, M, AFFINE, CH><<<static_cast<unsigned>(grid), 64 * kWaves, 0, b.stream>>>(
+                        static_cast<u32x4*>(b.dx->data), dwp, static_cast<const u32x4*>(dy),
+                        static_cast<const u32x4*>(b.x->data),
+                        static_cast<const u32x4*>(AFFINE ? b.w->data : b.x->data),
+                        static_cast<const float*>(b.rstd->data), static_cast<uint32_t>(b.rows), nvec,
+                        static_cast<uint32_t>(b.blocks), 1.0f / static_cast<float>(b.n), b.offset);
+                };
+                const uint32_t chunks = (nvec + 63) / 64;
+                if (chunks <= 1) go(std::integral_constant<int, 1>{});
+                else if (chunks <= 2) go(std::integral_constant<int, 2>{});
+                else if (chunks <= 4) go(std::integral_constant<int, 4>{});
+                else go(std::integral_constant<int, 8>{});
+                check_launch("launch rms_norm_bwd");
+                return;
+            }
+        }
         rms_bwd_block<X, W, M, AFFINE><<<static_cast<unsigned>(b.blocks), block_threads(b.n), 0, b.stream>>>(
             static_cast<X*>(b.dx->data), dwp, static_cast<const X*>(dy),
             static_cast<const X*>(b.x->data), static_cast<const W*>(AFFINE ? b.w->data : b.x->data),
