@@ -266,8 +266,9 @@ __global__ void __launch_bounds__(1024) rms_bwd_block(X* dx, float* __restrict__
 // [part * per, (part + 1) * per), reads each row's dy and x once with 16-byte
 // loads (CHUNKS vectors per lane), and keeps the row's fp32 dw contributions in
 // registers, summed over its rows in order. Same arithmetic and rounding points
-// as rms_bwd_block. Requires W == X (16-bit), n % 8 == 0 and 16-byte aligned
-// tensors. dy may alias dx (each row is read whole before it is written).
+// as rms_bwd_block. Requires 16-bit x, a weight of x's type or f32, n % 8 == 0
+// and 16-byte aligned tensors. dy may alias dx (each row is read whole before
+// it is written).
 template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
 __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __restrict__ dw_partial,
                                                            const u32x4* dy, const u32x4* __restrict__ x,
@@ -277,6 +278,8 @@ __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __
                                                            float offset) {
     constexpr int VEC = vec_of<X>();
     static_assert(VEC == 8, "16-bit element types");
+    // f32 weight: two 16-byte weight vectors per x vector.
+    constexpr int WPV = sizeof(typename Elem<W>::storage) == 4 ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const uint32_t part = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (part >= parts) return;
@@ -284,14 +287,25 @@ __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __
     const uint64_t r0 = static_cast<uint64_t>(part) * per;
     const uint64_t r1 = r0 + per < rows ? r0 + per : rows;
 
-    u32x4 wv[CHUNKS];
+    u32x4 wv[CHUNKS * WPV];
     if constexpr (AFFINE) {
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
             const uint32_t v = lane + 64u * c;
-            if (v < nvec) wv[c] = weight[v];
+#pragma unroll
+            for (int h = 0; h < WPV; ++h) {
+                if (v < nvec) wv[c * WPV + h] = weight[v * WPV + h];
+            }
         }
     }
+    auto widen_w = [&](int c, float* wf) __attribute__((always_inline)) {
+        if constexpr (WPV == 2) {
+            widen16<float>(wv[2 * c], wf);
+            widen16<float>(wv[2 * c + 1], wf + 4);
+        } else {
+            widen16<W>(wv[c], wf);
+        }
+    };
     float acc[AFFINE ? CHUNKS * VEC : 1];
 #pragma unroll
     for (int i = 0; i < (AFFINE ? CHUNKS * VEC : 1); ++i) acc[i] = 0.0f;
@@ -316,7 +330,7 @@ __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __
                 float g[VEC], xf[VEC], wf[VEC];
                 widen16<X>(gv[c], g);
                 widen16<X>(xv[c], xf);
-                if constexpr (AFFINE) widen16<W>(wv[c], wf);
+                if constexpr (AFFINE) widen_w(c, wf);
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) dot += (AFFINE ? g[e] * (wf[e] + offset) : g[e]) * xf[e];
             }
@@ -330,7 +344,7 @@ __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __
                 float g[VEC], xf[VEC], wf[VEC], o[VEC];
                 widen16<X>(gv[c], g);
                 widen16<X>(xv[c], xf);
-                if constexpr (AFFINE) widen16<W>(wv[c], wf);
+                if constexpr (AFFINE) widen_w(c, wf);
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
                     const float gg = AFFINE ? g[e] * (wf[e] + offset) : g[e];
@@ -569,7 +583,8 @@ struct BwdLaunch {
         // Without dy the gradient is read from dx (in place).
         const void* dy = b.dy ? b.dy->data : b.dx->data;
         float* dwp = AFFINE ? static_cast<float*>(b.dw_partial->data) : nullptr;
-        constexpr bool kWaveForm = vec_of<X>() == 8 && (!AFFINE || std::is_same<W, X>::value);
+        constexpr bool kWaveForm =
+            vec_of<X>() == 8 && (!AFFINE || std::is_same<W, X>::value || std::is_same<W, float>::value);
         if constexpr (kWaveForm) {
             const bool aligned = aligned16(b.dx->data) && aligned16(dy) && aligned16(b.x->data) &&
                                  (!AFFINE || (aligned16(b.w->data) && aligned16(dwp)));
