@@ -310,17 +310,25 @@ __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __
 #pragma unroll
     for (int i = 0; i < (AFFINE ? CHUNKS * VEC : 1); ++i) acc[i] = 0.0f;
 
-    for (uint64_t row = r0; row < r1; ++row) {
+    // The next row's dy and x are loaded before the current row is reduced and
+    // written (a different row, so this holds with dy aliasing dx too).
+    auto load_row = [&](uint64_t row, u32x4 (&g)[CHUNKS], u32x4 (&xr)[CHUNKS]) __attribute__((always_inline)) {
         const uint64_t base = row * nvec;
-        u32x4 gv[CHUNKS], xv[CHUNKS];
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
             const uint32_t v = lane + 64u * c;
             if (v < nvec) {
-                gv[c] = dy[base + v];
-                xv[c] = __builtin_nontemporal_load(x + base + v);
+                g[c] = dy[base + v];
+                xr[c] = __builtin_nontemporal_load(x + base + v);
             }
         }
+    };
+    u32x4 gv[CHUNKS], xv[CHUNKS];
+    if (r0 < r1) load_row(r0, gv, xv);
+    for (uint64_t row = r0; row < r1; ++row) {
+        const uint64_t base = row * nvec;
+        u32x4 gn[CHUNKS], xn[CHUNKS];
+        if (row + 1 < r1) load_row(row + 1, gn, xn);
         const float r = rstd[row];
         float dot = 0.0f;
 #pragma unroll
@@ -357,6 +365,11 @@ __global__ void __launch_bounds__(64 * kWaves) rms_bwd_wave(u32x4* dx, float* __
                 }
                 __builtin_nontemporal_store(narrow16<X>(o), dx + base + v);
             }
+        }
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            gv[c] = gn[c];
+            xv[c] = xn[c];
         }
     }
     if constexpr (AFFINE) {
