@@ -92,7 +92,7 @@ def wl_rmsnorm_bwd():
 
     # Algorithmic: read x, dy, w, rstd; write dx, dw (the partials are overhead).
     bytes_ = rows * n * 2 * 3 + n * 2 * 2 + rows * 4
-    return dict(run=run, work=bytes_, bound="hbm", kernel="rms_bwd_block",
+    return dict(run=run, work=bytes_, bound="hbm", kernel="rms_bwd_wave",
                 config={"x": [rows, n], "dtype": "bf16", "casting_mode": "llama"}, cpu=None)
 
 
@@ -108,7 +108,7 @@ def wl_silu():
     def run():
         activation_rs.ops.silu(out, x)
 
-    return dict(run=run, work=2 * x.numel() * 2, bound="hbm", kernel="activation_vec",
+    return dict(run=run, work=2 * x.numel() * 2, bound="hbm", kernel="activation_lut",
                 config={"x": list(x.shape), "dtype": "bf16"}, cpu=None)
 
 
@@ -126,7 +126,7 @@ def _wl_gated(op):
             fn(out, x)
 
         bytes_ = tokens * d2 * 2 + tokens * (d2 // 2) * 2
-        return dict(run=run, work=bytes_, bound="hbm", kernel="act_and_mul_vec",
+        return dict(run=run, work=bytes_, bound="hbm", kernel="act_and_mul_lut",
                     config={"x": [tokens, d2], "out": [tokens, d2 // 2], "dtype": "bf16"},
                     cpu=lambda: cpu_gated(op, x))
 

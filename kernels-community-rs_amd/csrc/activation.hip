@@ -15,9 +15,20 @@
 // rounded to the element type, then the product is formed in f32 and rounded
 // again (activation.rs:42-46, element.rs:103-106). The element-wise GELU
 // variants round at every step where the reference does (activation.rs:79-104).
+//
+// 16-bit element types: an activation of a bf16 / f16 input has only 65536
+// possible arguments, so each one is a 128 KB table of result bits, built once
+// per device with the reference's expression and correctly rounded f32 values
+// of exp / erf / tanh (evaluated in f64). The streaming kernels copy the table
+// into LDS (gfx950 has 160 KB per CU, so one 1024-thread block per CU holds it)
+// and replace the transcendental arithmetic by one LDS read per element. The
+// results are the table's, bit for bit, whichever kernel runs; the product with
+// the other half is exact in f32 and rounded once, as in the reference.
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 namespace kcr {
 
@@ -31,76 +42,18 @@ enum Act : int {
     ACT_FATRELU = 6,
 };
 
+// f32 -> T -> f32, from the rounded f32 value (the reference's order).
 template <typename T>
 __device__ __forceinline__ float rnd(float v) {
-    return Elem<T>::round(v);
+    return Elem<T>::round(as_f32(v));
 }
 
-// exp(x) for x in [-150, 80]: exp2 of the product x * log2(e) split into a
-// rounded head and its exact residual (the head via one multiply, the residual
-// via two FMAs against the two-float log2(e)), then one first-order correction
-// e * (1 + residual * ln 2). Relative error about 1 ulp of f32 (v_exp_f32's own).
-__device__ __forceinline__ float exp_split(float x) {
-    constexpr float kLog2eHi = 1.44269502162933349609375f;  // float(log2 e)
-    constexpr float kLog2eLo = 1.9259629911266175e-8f;      // log2 e - kLog2eHi
-    constexpr float kLn2f = 0.693147180559945309f;
-    const float h = x * kLog2eHi;
-    const float lo = __builtin_fmaf(x, kLog2eLo, __builtin_fmaf(x, kLog2eHi, -h));
-    const float e2 = __builtin_amdgcn_exp2f(h);
-    return __builtin_fmaf(e2 * lo, kLn2f, e2);
-}
-
-// f / (1 + exp(-z)) for z > -80 (so 1 + exp(-z) < 2^116 and its reciprocal is
-// a normal float) and finite f below 2^64: hardware reciprocal plus one Newton-Raphson correction of the
-// quotient, within about 1 ulp of the IEEE quotient. Used for 16-bit element
-// types, whose results are rounded to 8 or 11 significant bits afterwards.
-__device__ __forceinline__ float div_one_plus_exp_neg(float f, float z) {
-    const float d = 1.0f + exp_split(fmaxf(-z, -150.0f));
-    const float r = __builtin_amdgcn_rcpf(d);
-    const float q0 = f * r;
-    return __builtin_fmaf(__builtin_fmaf(-d, q0, f), r, q0);
-}
-
-// tanh(u) = sign(u) (1 - s), s = 2e / (1 + e), e = exp(-2|u|) in (0, 1], with
-// e = exp2(-2|u| log2 e) and the hardware reciprocal. The errors of e and s
-// (a few f32 ulp, relative) reach 1 - s only as s times that, below half an ulp
-// of 1 wherever s is small (|u| large, where 1 + tanh(u) cancels), so the
-// reference's rounding of tanh and of 1 + tanh is reproduced there. Infinite u
-// gives +-1; NaN u gives +-1 and the callers' products with the NaN input stay
-// NaN.
-__device__ __forceinline__ float tanh_lite(float u) {
-    constexpr float kNeg2Log2e = -2.0f * 1.44269502162933349609375f;
-    const float e = __builtin_amdgcn_exp2f(fmaxf(fabsf(u) * kNeg2Log2e, -300.0f));
-    const float s = e * __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, e, 0.5f));  // 2e / (1 + e)
-    return copysignf(1.0f - s, u);
-}
-
-// Whether the split-exp forms may stand in for the libm expression: 16-bit
-// element types only (their results keep 8 or 11 significant bits).
+// The f32 expression of activation A (activation.rs:42-122) with the device
+// libm; used for f32 elements (16-bit elements read tables, below).
 template <typename T, int A>
-constexpr bool has_fast_form() {
-    // gelu_tanh: bf16 only; f16's 11-bit results near the cancellation of
-    // 1 + tanh(u) resolve the few-ulp error of the exp2 / reciprocal form.
-    return (sizeof(typename Elem<T>::storage) == 2 && A == ACT_SILU) ||
-           (std::is_same<T, bf16_t>::value && A == ACT_GELU_TANH);
-}
-
-// Inputs the fast SiLU form covers: the split exp needs -f < 80 (no overflow of
-// 1 + exp(-f), normal reciprocal), the Newton step a finite f below 2^64. The
-// tails (and NaN) keep the reference expression.
-template <int A>
-__device__ __forceinline__ bool fast_form_covers(float f) {
-    if constexpr (A == ACT_SILU) return f > -80.0f && f < 0x1p64f;
-    return true;
-}
-
-template <typename T, int A, bool FAST = false>
 __device__ __forceinline__ float apply_act(float f, float threshold) {
-    constexpr bool kFast = FAST && has_fast_form<T, A>();
     if constexpr (A == ACT_SILU) {
-        // activation.rs:42-46: f / (1 + exp(-f)); the fast form is the split exp
-        // and a refined reciprocal (callers check fast_form_covers first).
-        if constexpr (kFast) return rnd<T>(div_one_plus_exp_neg(f, f));
+        // activation.rs:42-46: f / (1 + exp(-f))
         return rnd<T>(f / (1.0f + expf(-f)));
     } else if constexpr (A == ACT_GELU) {
         // activation.rs:53-58: f * 0.5 * (1 + erf(f / sqrt(2)))
@@ -113,9 +66,6 @@ __device__ __forceinline__ float apply_act(float f, float threshold) {
         const float kappa = 0.044715f;
         const float x_cube = f * f * f;
         const float inner = beta * __builtin_fmaf(kappa, x_cube, f);
-        // bf16: tanh from one exp2 and one reciprocal (tanh_lite), then
-        // the reference's own 1 + tanh(u) and products.
-        if constexpr (kFast) return rnd<T>(0.5f * f * (1.0f + tanh_lite(inner)));
         return rnd<T>(0.5f * f * (1.0f + tanhf(inner)));
     } else if constexpr (A == ACT_GELU_NEW) {
         // activation.rs:79-90, every intermediate in T.
@@ -138,12 +88,121 @@ __device__ __forceinline__ float apply_act(float f, float threshold) {
     }
 }
 
-template <typename T, int A, bool ACT_FIRST, bool FAST = false>
+// ---------------------------------------------------------------------------
+// Exact activations of 16-bit inputs, and their tables.
+// ---------------------------------------------------------------------------
+
+// Correctly rounded f32 values of the elementary functions: the f64 result
+// (accurate to about one f64 ulp) rounded once to f32.
+__device__ __forceinline__ float exp_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+__device__ __forceinline__ float erf_cr(float x) { return static_cast<float>(erf(static_cast<double>(x))); }
+__device__ __forceinline__ float tanh_cr(float x) { return static_cast<float>(tanh(static_cast<double>(x))); }
+// IEEE f32 quotient: the f64 quotient of two floats rounds to the same float.
+__device__ __forceinline__ float div_rn(float a, float b) {
+    return static_cast<float>(static_cast<double>(a) / static_cast<double>(b));
+}
+
+// The reference's expression for A (activation.rs:42-115) with every f32
+// operation rounded separately (no contraction) and the elementary functions
+// correctly rounded; returns the result rounded to T.
+template <typename T, int A>
+__device__ float act_exact(float f) {
+#pragma clang fp contract(off)
+    if constexpr (A == ACT_SILU) {
+        return rnd<T>(div_rn(f, 1.0f + exp_cr(-f)));
+    } else if constexpr (A == ACT_GELU) {
+        const float alpha = 0.70710678118654752440f;
+        return rnd<T>(f * 0.5f * (1.0f + erf_cr(f * alpha)));
+    } else if constexpr (A == ACT_GELU_TANH) {
+        const float beta = static_cast<float>(1.4142135623730951 * 1.1283791670955126 * 0.5);
+        const float kappa = 0.044715f;
+        const float x_cube = f * f * f;
+        const float inner = beta * __builtin_fmaf(kappa, x_cube, f);
+        return rnd<T>(0.5f * f * (1.0f + tanh_cr(inner)));
+    } else if constexpr (A == ACT_GELU_NEW) {
+        const float x3 = rnd<T>(rnd<T>(f * f) * f);
+        const float inner = rnd<T>(f + rnd<T>(0.044715f * x3));
+        const float t = rnd<T>(tanh_cr(rnd<T>(0.79788456f * inner)));
+        return rnd<T>(rnd<T>(rnd<T>(0.5f) * f) * rnd<T>(rnd<T>(1.0f) + t));
+    } else if constexpr (A == ACT_GELU_FAST) {
+        const float scaled = rnd<T>(f * 0.79788456f);
+        const float cubic = rnd<T>(rnd<T>(1.0f) + rnd<T>(rnd<T>(0.044715f * f) * f));
+        const float t = rnd<T>(tanh_cr(rnd<T>(scaled * cubic)));
+        return rnd<T>(rnd<T>(rnd<T>(0.5f) * f) * rnd<T>(rnd<T>(1.0f) + t));
+    } else {
+        static_assert(A == ACT_GELU_QUICK, "activations with a table");
+        return rnd<T>(div_rn(f, 1.0f + exp_cr(-1.702f * f)));
+    }
+}
+
+// Table slots: [dtype (0 bf16, 1 f16)][activation], 65536 result bits each.
+constexpr int kLutActs = 6;  // ACT_SILU .. ACT_GELU_QUICK
+template <int A>
+constexpr bool has_lut() {
+    return A >= ACT_SILU && A <= ACT_GELU_QUICK;
+}
+template <typename T>
+constexpr int lut_dtype() {
+    return std::is_same<T, bf16_t>::value ? 0 : 1;
+}
+template <typename T, int A>
+constexpr int lut_slot() {
+    return lut_dtype<T>() * kLutActs + A;
+}
+
+// 12 x 128 KB in device memory, filled by build_act_luts once per device.
+__device__ uint16_t g_act_lut[2 * kLutActs][65536];
+
+template <typename T>
+__device__ void fill_lut_entry(int act, uint32_t bits) {
+    const float f = Elem<T>::to_f32(bits);
+    uint32_t r;
+    switch (act) {
+        case ACT_SILU: r = Elem<T>::from_f32(act_exact<T, ACT_SILU>(f)); break;
+        case ACT_GELU: r = Elem<T>::from_f32(act_exact<T, ACT_GELU>(f)); break;
+        case ACT_GELU_TANH: r = Elem<T>::from_f32(act_exact<T, ACT_GELU_TANH>(f)); break;
+        case ACT_GELU_NEW: r = Elem<T>::from_f32(act_exact<T, ACT_GELU_NEW>(f)); break;
+        case ACT_GELU_FAST: r = Elem<T>::from_f32(act_exact<T, ACT_GELU_FAST>(f)); break;
+        default: r = Elem<T>::from_f32(act_exact<T, ACT_GELU_QUICK>(f)); break;
+    }
+    g_act_lut[lut_dtype<T>() * kLutActs + act][bits] = static_cast<uint16_t>(r);
+}
+
+// One thread per (table, input): grid 2 * kLutActs * 256 blocks of 256.
+__global__ void __launch_bounds__(256) build_act_luts() {
+    const uint32_t id = blockIdx.x * 256u + threadIdx.x;
+    const int slot = static_cast<int>(id >> 16);
+    const uint32_t bits = id & 0xffffu;
+    if (slot < kLutActs) {
+        fill_lut_entry<bf16_t>(slot, bits);
+    } else if (slot < 2 * kLutActs) {
+        fill_lut_entry<f16_t>(slot - kLutActs, bits);
+    }
+}
+
+// Result bits of activation A at 16-bit input bits, from the global table
+// (the scalar kernels; the streaming kernels read their LDS copy).
+template <typename T, int A>
+__device__ __forceinline__ float act_lut_global(uint32_t bits) {
+    return Elem<T>::to_f32(g_act_lut[lut_slot<T, A>()][bits]);
+}
+
+// act(f) rounded to T: the table for 16-bit T, else the f32 expression.
+template <typename T, int A>
+__device__ __forceinline__ float act_value(float f, float threshold) {
+    if constexpr (sizeof(typename Elem<T>::storage) == 2 && has_lut<A>()) {
+        return act_lut_global<T, A>(Elem<T>::from_f32(f));
+    } else {
+        return apply_act<T, A>(f, threshold);
+    }
+}
+
+template <typename T, int A, bool ACT_FIRST>
 __device__ __forceinline__ float gated(float x, float y, float threshold) {
     if constexpr (ACT_FIRST) {
-        return apply_act<T, A, FAST>(x, threshold) * y;
+        return act_value<T, A>(x, threshold) * y;
     } else {
-        return x * apply_act<T, A, FAST>(y, threshold);
+        return x * act_value<T, A>(y, threshold);
     }
 }
 
@@ -231,18 +290,8 @@ __global__ void __launch_bounds__(kThreads) act_and_mul_vec(u32x4* __restrict__ 
             float x[VEC], y[VEC], r[VEC];
             widen<T>(xs[u], x);
             widen<T>(ys[u], y);
-            // One branch per vector: the fast form when it covers every element
-            // of this lane's vector (always, for ordinary data).
-            bool fast = has_fast_form<T, A>();
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) fast = fast && fast_form_covers<A>(ACT_FIRST ? x[e] : y[e]);
-            if (fast) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) r[e] = gated<T, A, ACT_FIRST, true>(x[e], y[e], threshold);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) r[e] = gated<T, A, ACT_FIRST>(x[e], y[e], threshold);
-            }
+            for (int e = 0; e < VEC; ++e) r[e] = gated<T, A, ACT_FIRST>(x[e], y[e], threshold);
             __builtin_nontemporal_store(narrow<T>(r), out + oidx[u]);
         }
     }
@@ -262,7 +311,8 @@ __global__ void __launch_bounds__(kThreads) act_and_mul_scalar(T* __restrict__ o
         const uint64_t col = i - row * d;
         const float x = Elem<T>::load(in + row * 2 * d + col);
         const float y = Elem<T>::load(in + row * 2 * d + d + col);
-        Elem<T>::store(out + i, gated<T, A, ACT_FIRST>(x, y, threshold));
+        Elem<T>::store(out + i, ACT_FIRST ? act_value<T, A>(x, threshold) * y
+                                          : x * act_value<T, A>(y, threshold));
     }
 }
 
@@ -288,19 +338,113 @@ __global__ void __launch_bounds__(kThreads) activation_vec(u32x4* __restrict__ o
             if (j >= total) continue;
             float x[VEC], r[VEC];
             widen<T>(xs[u], x);
-            // The fast activation forms of the gated kernel, under the same
-            // per-vector coverage check.
-            bool fast = has_fast_form<T, A>();
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) fast = fast && fast_form_covers<A>(x[e]);
-            if (fast) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) r[e] = apply_act<T, A, true>(x[e], 0.0f);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) r[e] = apply_act<T, A>(x[e], 0.0f);
-            }
+            for (int e = 0; e < VEC; ++e) r[e] = act_value<T, A>(x[e], 0.0f);
             __builtin_nontemporal_store(narrow<T>(r), out + j);
+        }
+    }
+}
+
+// Streaming kernels over a table in LDS. A block is 1024 threads (the 128 KB
+// table leaves no room for a second block on the CU), each thread U 16-byte
+// vectors of each input per iteration. Measured on MI355X (silu_and_mul,
+// 16384 x 28672 bf16): a grid that covers the input in one pass (every block
+// one iteration, blocks dispatched as CUs free up) streams at 6.35-6.39 TB/s;
+// capping the grid at 1, 4 or 16 blocks per CU and looping gave 5.54, 5.79
+// and 6.06 TB/s: the dispatcher's dynamic balance across CUs is worth more
+// than the 128 KB table copy each block makes from L2. The element-wise
+// kernels (one input) run best with U = 2 and at most 24 blocks per CU
+// (6.12 TB/s against 5.65 for one pass at U = 4).
+constexpr int kLutThreads = 1024;
+constexpr int kGatedLutUnroll = 4;
+constexpr int kEltLutUnroll = 2;
+constexpr int kEltLutBlocksPerCu = 24;
+
+// Copies table `slot` into `lut` (128 KB of LDS) and waits for the block.
+__device__ __forceinline__ void load_lut(uint16_t* lut, int slot) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(g_act_lut[slot]);
+    u32x4* dst = reinterpret_cast<u32x4*>(lut);
+#pragma unroll
+    for (int i = 0; i < 65536 * 2 / 16 / kLutThreads; ++i) dst[threadIdx.x + i * kLutThreads] = src[threadIdx.x + i * kLutThreads];
+    __syncthreads();
+}
+
+template <typename T, int A, bool ACT_FIRST, bool WIDE>
+__global__ void __launch_bounds__(kLutThreads) act_and_mul_lut(u32x4* __restrict__ out,
+                                                               const u32x4* __restrict__ in,
+                                                               uint64_t total, uint32_t vpr) {
+    constexpr int U = kGatedLutUnroll;
+    __shared__ uint16_t lut[65536];
+    load_lut(lut, lut_slot<T, A>());
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kLutThreads * U;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kLutThreads * U + threadIdx.x; i < total;
+         i += stride) {
+        u32x4 xs[U], ys[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * kLutThreads;
+            uint64_t row, col;
+            if constexpr (WIDE) {
+                row = j / vpr;
+                col = j - row * vpr;
+            } else {
+                const uint32_t j32 = static_cast<uint32_t>(j);
+                row = j32 / vpr;
+                col = j32 - static_cast<uint32_t>(row) * vpr;
+            }
+            const uint64_t base = row * 2 * vpr + col;
+            if (j < total) {
+                xs[u] = __builtin_nontemporal_load(in + base);
+                ys[u] = __builtin_nontemporal_load(in + base + vpr);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * kLutThreads;
+            if (j >= total) continue;
+            u32x4 r;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // a: the half the activation applies to; b: the other half.
+                const uint32_t a = ACT_FIRST ? xs[u][k] : ys[u][k];
+                const uint32_t b = ACT_FIRST ? ys[u][k] : xs[u][k];
+                const float al = Elem<T>::to_f32(lut[a & 0xffffu]);
+                const float ah = Elem<T>::to_f32(lut[a >> 16]);
+                // Products of two 16-bit values are exact in f32: one rounding.
+                r[k] = pack_pair<T>(al * Elem<T>::to_f32(b & 0xffffu), ah * Elem<T>::to_f32(b >> 16));
+            }
+            __builtin_nontemporal_store(r, out + j);
+        }
+    }
+}
+
+// Element-wise: out = table[in], no arithmetic at all.
+template <typename T, int A>
+__global__ void __launch_bounds__(kLutThreads) activation_lut(u32x4* __restrict__ out,
+                                                              const u32x4* __restrict__ in,
+                                                              uint64_t total) {
+    constexpr int U = kEltLutUnroll;
+    __shared__ uint16_t lut[65536];
+    load_lut(lut, lut_slot<T, A>());
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kLutThreads * U;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kLutThreads * U + threadIdx.x; i < total;
+         i += stride) {
+        u32x4 xs[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * kLutThreads;
+            if (j < total) xs[u] = __builtin_nontemporal_load(in + j);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * kLutThreads;
+            if (j >= total) continue;
+            u32x4 r;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                r[k] = static_cast<uint32_t>(lut[xs[u][k] & 0xffffu]) |
+                       (static_cast<uint32_t>(lut[xs[u][k] >> 16]) << 16);
+            __builtin_nontemporal_store(r, out + j);
         }
     }
 }
@@ -312,7 +456,7 @@ __global__ void __launch_bounds__(kThreads) activation_scalar(T* __restrict__ ou
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
          i += stride) {
-        Elem<T>::store(out + i, apply_act<T, A>(Elem<T>::load(in + i), 0.0f));
+        Elem<T>::store(out + i, act_value<T, A>(Elem<T>::load(in + i), 0.0f));
     }
 }
 
@@ -327,6 +471,36 @@ unsigned grid_for(uint64_t work_items) {
     if (blocks > cap) blocks = cap;
     if (blocks == 0) blocks = 1;
     return static_cast<unsigned>(blocks);
+}
+
+// Builds the activation tables of the current device on its first use (one
+// kernel on a private stream, waited for, so the tables are complete before
+// any stream of the caller reads them). Later calls return at once.
+void ensure_luts() {
+    static std::mutex mu;
+    static std::vector<char> built;
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    if (static_cast<size_t>(device) < built.size() && built[device]) return;
+    hipStream_t s;
+    check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    build_act_luts<<<2 * kLutActs * 256, 256, 0, s>>>();
+    const hipError_t launched = hipGetLastError();
+    const hipError_t done = hipStreamSynchronize(s);
+    hipStreamDestroy(s);
+    check_hip(launched, "launch build_act_luts");
+    check_hip(done, "build_act_luts");
+    if (built.size() <= static_cast<size_t>(device)) built.resize(device + 1, 0);
+    built[device] = 1;
+}
+
+// Grid of a table kernel: enough blocks of kLutThreads x unroll vectors to
+// cover the input once, at most `cap`.
+unsigned lut_grid(uint64_t total_vectors, int unroll, uint64_t cap) {
+    const uint64_t per_block = static_cast<uint64_t>(kLutThreads) * unroll;
+    const uint64_t need = (total_vectors + per_block - 1) / per_block;
+    return static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, cap)));
 }
 
 struct Launch {
@@ -389,12 +563,30 @@ void launch_gated_t(const kcr_tensor* out, const kcr_tensor* input, const Launch
     if (vec) {
         const uint64_t vpr = static_cast<uint64_t>(l.d) / VEC;
         const uint64_t total = static_cast<uint64_t>(l.tokens) * vpr;
+        if constexpr (sizeof(typename Elem<T>::storage) == 2 && has_lut<A>()) {
+            ensure_luts();
+            const unsigned grid = lut_grid(total, kGatedLutUnroll, 2147483647ull);
+            // 32-bit index math when every flat index, plus one grid stride of
+            // unrolled look-ahead, stays below 2^32.
+            const uint64_t reach = total + static_cast<uint64_t>(grid) * kLutThreads * kGatedLutUnroll;
+            if (reach < (1ull << 32)) {
+                act_and_mul_lut<T, A, ACT_FIRST, false><<<grid, kLutThreads, 0, stream>>>(
+                    static_cast<u32x4*>(out->data), static_cast<const u32x4*>(input->data), total,
+                    static_cast<uint32_t>(vpr));
+            } else {
+                act_and_mul_lut<T, A, ACT_FIRST, true><<<grid, kLutThreads, 0, stream>>>(
+                    static_cast<u32x4*>(out->data), static_cast<const u32x4*>(input->data), total,
+                    static_cast<uint32_t>(vpr));
+            }
+            check_launch("launch act_and_mul");
+            return;
+        }
         const uint64_t need = (total + kThreads * kGatedUnroll - 1) / (kThreads * kGatedUnroll);
         const unsigned grid = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(need, kGatedBlocks)));
-        // 32-bit index math is enough when every flat index (plus one grid
-        // stride of unrolled look-ahead) fits below 2^32.
-        const uint64_t reach = total + static_cast<uint64_t>(grid) * kThreads * kUnroll;
-        if (reach < (1ull << 32) && vpr < (1ull << 32)) {
+        // 32-bit index math when every flat index, plus one grid stride of
+        // unrolled look-ahead, stays below 2^32.
+        const uint64_t reach = total + static_cast<uint64_t>(grid) * kThreads * kGatedUnroll;
+        if (reach < (1ull << 32)) {
             act_and_mul_vec<T, A, ACT_FIRST, false><<<grid, kThreads, 0, stream>>>(
                 static_cast<u32x4*>(out->data), static_cast<const u32x4*>(input->data), total,
                 static_cast<uint32_t>(vpr), threshold);
@@ -404,6 +596,7 @@ void launch_gated_t(const kcr_tensor* out, const kcr_tensor* input, const Launch
                 static_cast<uint32_t>(vpr), threshold);
         }
     } else {
+        if constexpr (sizeof(typename Elem<T>::storage) == 2 && has_lut<A>()) ensure_luts();
         const unsigned grid = grid_for(total_elems);
         act_and_mul_scalar<T, A, ACT_FIRST><<<grid, kThreads, 0, stream>>>(
             static_cast<T*>(out->data), static_cast<const T*>(input->data), total_elems,
@@ -432,8 +625,18 @@ void launch_elementwise_t(const kcr_tensor* out, const kcr_tensor* input, const 
                           hipStream_t stream) {
     constexpr int VEC = vec_elems<T>();
     const uint64_t total_elems = static_cast<uint64_t>(l.tokens) * static_cast<uint64_t>(l.d);
+    constexpr bool kTable = sizeof(typename Elem<T>::storage) == 2 && has_lut<A>();
+    if constexpr (kTable) ensure_luts();
     if (total_elems % VEC == 0 && aligned16(out->data) && aligned16(input->data)) {
         const uint64_t total = total_elems / VEC;
+        if constexpr (kTable) {
+            const unsigned grid = lut_grid(total, kEltLutUnroll,
+                                           static_cast<uint64_t>(kEltLutBlocksPerCu) * compute_units());
+            activation_lut<T, A><<<grid, kLutThreads, 0, stream>>>(
+                static_cast<u32x4*>(out->data), static_cast<const u32x4*>(input->data), total);
+            check_launch("launch activation");
+            return;
+        }
         const uint64_t need = (total + kThreads * kGatedUnroll - 1) / (kThreads * kGatedUnroll);
         const unsigned grid = static_cast<unsigned>(std::max<uint64_t>(1, std::min(need, kGatedBlocks)));
         activation_vec<T, A><<<grid, kThreads, 0, stream>>>(

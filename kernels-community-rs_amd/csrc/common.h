@@ -185,6 +185,16 @@ struct Elem<f16_t> {
     static __device__ __forceinline__ float round(float v) { return to_f32(from_f32(v)); }
 };
 
+// A value the compiler must materialise as an f32 before its next use. An
+// f32 result narrowed to f16 is otherwise folded into one mixed-precision
+// instruction (v_fma_mixlo_f16) that rounds the exact result to f16 once,
+// where an f32 computation rounds to f32 first and then to f16 (the two differ
+// at f16 ties of the f32 value). Used where results must match that order.
+__device__ __forceinline__ float as_f32(float v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 // 16-byte vectors of 8 x 16-bit or 4 x 32-bit elements.
 using u32x4 = __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t;
 

@@ -19,6 +19,11 @@
 
 #include <type_traits>
 
+// The reference's f32 arithmetic is never fused (Rust does not contract a
+// multiply and an add into an FMA), and results such as mean(x^2) + eps, i.e.
+// sum * (1/n) + eps, depend on it: no contraction anywhere in this file.
+#pragma clang fp contract(off)
+
 namespace kcr {
 
 enum Mode : int { MODE_LLAMA = 0, MODE_GEMMA = 1, MODE_NONE = 2 };
@@ -31,9 +36,16 @@ struct Casting {
     static constexpr bool round_weight_grad = (M == MODE_LLAMA);
 };
 
+// f32 -> T -> f32, from the rounded f32 value.
 template <typename T>
 __device__ __forceinline__ float rnd(float v) {
-    return Elem<T>::round(v);
+    return Elem<T>::round(as_f32(v));
+}
+
+// Stores an f32 result as T, from the rounded f32 value.
+template <typename T>
+__device__ __forceinline__ void store_rn(T* p, float v) {
+    Elem<T>::store(p, as_f32(v));
 }
 
 template <typename T>
@@ -64,19 +76,27 @@ __device__ __forceinline__ u32x4 narrow16(const float* f) {
         for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(f[i]);
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(f[2 * i], f[2 * i + 1]);
+        for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(as_f32(f[2 * i]), as_f32(f[2 * i + 1]));
     }
     return w;
 }
 
-// rstd = 1 / sqrt(mean(x^2) + eps), device.rs:147-153.
+// rstd = 1 / sqrt(mean(x^2) + eps), device.rs:147-153. mean(x^2) is the f32
+// product sum_sq * inv_n and the eps add is f32 as in the reference; the inverse
+// square root is evaluated in f64 and rounded once to f32, i.e. the correctly
+// rounded f32 value (the reference calls libdevice's rsqrtf, which approximates
+// that value).
+__device__ __forceinline__ float rsqrt_rn(float v) {
+    return static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(v)));
+}
+
 template <typename X, int M>
 __device__ __forceinline__ float row_rstd(float sum_sq, float inv_n, float eps) {
     const float mean_square = sum_sq * inv_n;
     if constexpr (Casting<M>::input_dtype_math) {
-        return rnd<X>(1.0f / sqrtf(rnd<X>(mean_square) + rnd<X>(eps)));
+        return rnd<X>(rsqrt_rn(rnd<X>(mean_square) + rnd<X>(eps)));
     } else {
-        return 1.0f / sqrtf(mean_square + eps);
+        return rsqrt_rn(mean_square + eps);
     }
 }
 
@@ -94,32 +114,119 @@ __device__ __forceinline__ float normalize(float x, float w, float rstd, float o
     }
 }
 
+// ---------------------------------------------------------------------------
+// The sum of squares of a row, in the reference's order.
+//
+// The reference (device.rs:41-63, 113-145) runs T = block_threads(n) threads
+// per row (ops.rs:98-106). With 16-byte access ("vectorized", ops.rs:108-115)
+// thread t owns the 8-element groups t, t + T, t + 2T, ... of the first
+// floor(n / 8) * 8 columns and then the single columns tail + t, tail + t + T,
+// ...; without it, the single columns t, t + T, .... Its partial is
+//   S(g0) + S(g1) + ... + x_c * x_c + ...,   S(g) = (((q0 + q1) + q2) ... + q7),
+// every product and sum rounded to f32 (no fused multiply-add). The partials
+// of each 32-thread warp are reduced by a butterfly with lane distances 16, 8,
+// 4, 2, 1, and the T / 32 warp sums by the same butterfly over 32 slots of
+// which the first T / 32 hold the sums (the rest zero). The kernels below
+// reproduce that order exactly, so the row's sum, rstd and y are the same bits
+// whichever kernel runs.
+// ---------------------------------------------------------------------------
+
+// One f32 product added to a running sum, rounded twice.
+__device__ __forceinline__ float add_square(float sum, float v) { return sum + v * v; }
+
+// S(g) of 8 widened values.
+__device__ __forceinline__ float group_squares(const float* f) {
+    float s = f[0] * f[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) s = s + f[i] * f[i];
+    return s;
+}
+
+// v + (value of the lane at distance D within the lane's 32-lane half).
+template <int D>
+__device__ __forceinline__ float add_xor32(float v) {
+    // ds_swizzle bit-mask mode: and_mask 0x1f, xor_mask D (within 32 lanes).
+    const int other = __builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (D << 10));
+    return v + __int_as_float(other);
+}
+
+// The 32-lane butterfly of one warp: every lane of a 32-lane half ends with
+// the half's sum in the reference's pairing.
+__device__ __forceinline__ float warp32_sum(float v) {
+    v = add_xor32<16>(v);
+    v = add_xor32<8>(v);
+    v = add_xor32<4>(v);
+    v = add_xor32<2>(v);
+    return add_xor32<1>(v);
+}
+
+// The block-level butterfly over NW warp sums (NW in {4, 8, 16, 32}): slots
+// NW..31 are zero and adding them changes nothing (the sums are >= +0), so the
+// steps with distance >= NW are skipped.
+template <int NW>
+__device__ __forceinline__ float warp_tree(float (&p)[NW]) {
+#pragma unroll
+    for (int d = NW / 2; d >= 1; d /= 2) {
+#pragma unroll
+        for (int i = 0; i < d; ++i) p[i] = p[i] + p[i + d];
+    }
+    return p[0];
+}
+
+// Widens the 8-element group at `p` (16-byte aligned) to f32.
+template <typename X>
+__device__ __forceinline__ void load_group(const X* p, float (&f)[8]) {
+    const u32x4* v = reinterpret_cast<const u32x4*>(p);
+    if constexpr (sizeof(typename Elem<X>::storage) == 4) {
+        widen16<float>(v[0], f);
+        widen16<float>(v[1], f + 4);
+    } else {
+        widen16<X>(v[0], f);
+    }
+}
+
+template <typename X>
+__device__ __forceinline__ void store_group(X* p, const float (&f)[8]) {
+    u32x4* v = reinterpret_cast<u32x4*>(p);
+    if constexpr (sizeof(typename Elem<X>::storage) == 4) {
+        v[0] = narrow16<float>(f);
+        v[1] = narrow16<float>(f + 4);
+    } else {
+        v[0] = narrow16<X>(f);
+    }
+}
+
 constexpr int kWaves = 4;  // waves per block of the wave-per-row kernel
 
-// One wave per row, the row held in registers: CHUNKS 16-byte vectors per lane.
-// Requires n % VEC_X == 0, 16-byte aligned tensors, and (with AFFINE) a weight
-// whose 16-byte vectors cover the same columns: W == X, or f32 weight read as
-// two 16-byte halves per x vector.
-template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
+// One wave per row, the row held in registers. Lane l holds the 8-element
+// groups l + 64 c (c < CHUNKS), each as 16 bytes (16-bit X) or 32 bytes (f32).
+// The reference thread owning group g is g mod T, so with SLOTS = T / 64 the
+// lane's group c belongs to thread l + 64 (c mod SLOTS), warp 2 (c mod SLOTS) +
+// (l >= 32): the lane keeps one partial per slot and the 32-lane butterflies
+// give the warp sums. Requires n % 8 == 0, 16-byte aligned tensors and (with
+// AFFINE) a weight of X's type or f32.
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS, int SLOTS>
 __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
-    u32x4* __restrict__ y, float* __restrict__ rstd_out, const u32x4* __restrict__ x,
-    const u32x4* __restrict__ weight, uint32_t rows, uint32_t nvec, float inv_n, float eps,
+    X* __restrict__ y, float* __restrict__ rstd_out, const X* __restrict__ x,
+    const W* __restrict__ weight, uint32_t rows, uint32_t groups, float inv_n, float eps,
     float offset) {
-    constexpr int VEC = vec_of<X>();
-    // f32 weight with 16-bit x: two 16-byte weight vectors per x vector.
-    constexpr int WPV = (sizeof(typename Elem<W>::storage) > sizeof(typename Elem<X>::storage)) ? 2 : 1;
+    constexpr int XV = sizeof(typename Elem<X>::storage) == 4 ? 2 : 1;  // 16-byte vectors per group
+    constexpr int WV = sizeof(typename Elem<W>::storage) == 4 ? 2 : 1;
+    constexpr int NW = 2 * SLOTS;
     const int lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const uint32_t waves = gridDim.x * kWaves;
+    const uint32_t n = groups * 8;
 
-    u32x4 wv[AFFINE ? CHUNKS * WPV : 1];
+    u32x4 wv[AFFINE ? CHUNKS * WV : 1];
     if constexpr (AFFINE) {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(weight);
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
-            const uint32_t v = lane + 64u * c;
+            const uint32_t g = lane + 64u * c;
 #pragma unroll
-            for (int h = 0; h < WPV; ++h) {
-                if (v < nvec) wv[c * WPV + h] = weight[v * WPV + h];
+            for (int h = 0; h < WV; ++h) {
+                if (g < groups) wv[c * WV + h] = wp[g * WV + h];
             }
         }
     }
@@ -127,42 +234,62 @@ __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
     // Rows are dealt to waves round-robin; the next row's loads are issued
     // before the current row is reduced and written, so every wave keeps a
     // whole row of reads in flight.
-    auto load_row = [&](uint32_t r, u32x4 (&dst)[CHUNKS]) {
-        const u32x4* xr = x + static_cast<uint64_t>(r) * nvec;
+    auto load_row = [&](uint32_t r, u32x4 (&dst)[CHUNKS * XV]) {
+        const u32x4* xr = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(r) * n);
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
-            const uint32_t v = lane + 64u * c;
-            if (v < nvec) dst[c] = __builtin_nontemporal_load(xr + v);
-        }
-    };
-    u32x4 xv[CHUNKS];
-    if (wave < rows) load_row(wave, xv);
-    for (uint32_t row = wave; row < rows; row += waves) {
-        u32x4 xn[CHUNKS];
-        if (row + waves < rows) load_row(row + waves, xn);
-        float sum = 0.0f;
+            const uint32_t g = lane + 64u * c;
 #pragma unroll
-        for (int c = 0; c < CHUNKS; ++c) {
-            const uint32_t v = lane + 64u * c;
-            if (v < nvec) {
-                float f[VEC];
-                widen16<X>(xv[c], f);
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) sum += f[e] * f[e];
+            for (int h = 0; h < XV; ++h) {
+                if (g < groups) dst[c * XV + h] = __builtin_nontemporal_load(xr + g * XV + h);
             }
         }
-        sum = wave_sum(sum);
-        const float rstd = row_rstd<X, M>(sum, inv_n, eps);
-        if (lane == 0) rstd_out[row] = rstd;
-        u32x4* yr = y + static_cast<uint64_t>(row) * nvec;
+    };
+    auto widen_x = [&](const u32x4 (&src)[CHUNKS * XV], int c, float (&f)[8]) {
+        if constexpr (XV == 2) {
+            widen16<float>(src[2 * c], f);
+            widen16<float>(src[2 * c + 1], f + 4);
+        } else {
+            widen16<X>(src[c], f);
+        }
+    };
+    u32x4 xv[CHUNKS * XV];
+    if (wave < rows) load_row(wave, xv);
+    for (uint32_t row = wave; row < rows; row += waves) {
+        u32x4 xn[CHUNKS * XV];
+        if (row + waves < rows) load_row(row + waves, xn);
+        float part[SLOTS];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) part[s] = 0.0f;
 #pragma unroll
         for (int c = 0; c < CHUNKS; ++c) {
-            const uint32_t v = lane + 64u * c;
-            if (v < nvec) {
-                float f[VEC], w[VEC], o[VEC];
-                widen16<X>(xv[c], f);
+            if (lane + 64u * c < groups) {
+                float f[8];
+                widen_x(xv, c, f);
+                part[c % SLOTS] = part[c % SLOTS] + group_squares(f);
+            }
+        }
+        // Warp sums: slot s of the lower half is warp 2s, of the upper half 2s + 1.
+        float ws[NW];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const float own = s < CHUNKS ? warp32_sum(part[s]) : 0.0f;
+            const float other = __shfl_xor(own, 32);
+            const bool upper = lane >= 32;
+            ws[2 * s] = upper ? other : own;
+            ws[2 * s + 1] = upper ? own : other;
+        }
+        const float rstd = row_rstd<X, M>(warp_tree<NW>(ws), inv_n, eps);
+        if (lane == 0) rstd_out[row] = rstd;
+        X* yr = y + static_cast<uint64_t>(row) * n;
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            const uint32_t g = lane + 64u * c;
+            if (g < groups) {
+                float f[8], w[8], o[8];
+                widen_x(xv, c, f);
                 if constexpr (AFFINE) {
-                    if constexpr (WPV == 2) {
+                    if constexpr (WV == 2) {
                         widen16<float>(wv[2 * c], w);
                         widen16<float>(wv[2 * c + 1], w + 4);
                     } else {
@@ -170,43 +297,65 @@ __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
                     }
                 }
 #pragma unroll
-                for (int e = 0; e < VEC; ++e)
+                for (int e = 0; e < 8; ++e)
                     o[e] = normalize<X, W, M, AFFINE>(f[e], AFFINE ? w[e] : 0.0f, rstd, offset);
-                __builtin_nontemporal_store(narrow16<X>(o), yr + v);
+                u32x4* yv = reinterpret_cast<u32x4*>(yr) + g * XV;
+                if constexpr (XV == 2) {
+                    __builtin_nontemporal_store(narrow16<float>(o), yv);
+                    __builtin_nontemporal_store(narrow16<float>(o + 4), yv + 1);
+                } else {
+                    __builtin_nontemporal_store(narrow16<X>(o), yv);
+                }
             }
         }
 #pragma unroll
-        for (int c = 0; c < CHUNKS; ++c) xv[c] = xn[c];
+        for (int c = 0; c < CHUNKS * XV; ++c) xv[c] = xn[c];
     }
 }
 
-// Block per row, scalar columns; two passes (the second mostly from L2).
-template <typename X, typename W, int M, bool AFFINE>
-__global__ void __launch_bounds__(1024) rms_fwd_block(X* __restrict__ y, float* __restrict__ rstd_out,
-                                                      const X* __restrict__ x,
-                                                      const W* __restrict__ weight, uint32_t n,
-                                                      float inv_n, float eps, float offset) {
-    __shared__ float partial[16];
+// Block per row with the reference's T = blockDim.x threads and its column
+// assignment (groups when `vectorized`, then single columns); two passes over
+// the row (the second mostly from L2). NW = T / 32 warp sums.
+template <typename X, typename W, int M, bool AFFINE, int NW>
+__global__ void __launch_bounds__(32 * NW) rms_fwd_block(X* __restrict__ y, float* __restrict__ rstd_out,
+                                                         const X* __restrict__ x,
+                                                         const W* __restrict__ weight, uint32_t n,
+                                                         uint32_t vectorized, float inv_n, float eps,
+                                                         float offset) {
+    __shared__ float warp_sums[NW];
+    constexpr uint32_t T = 32 * NW;
     const uint64_t row = blockIdx.x;
     const X* xr = x + row * n;
     X* yr = y + row * n;
+    const uint32_t t = threadIdx.x;
+    const uint32_t tail = vectorized ? n / 8 * 8 : 0;
     float sum = 0.0f;
-    for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) {
-        const float v = Elem<X>::load(xr + c);
-        sum += v * v;
+    for (uint32_t col = 8 * t; col < tail; col += 8 * T) {
+        float f[8];
+        load_group<X>(xr + col, f);
+        sum = sum + group_squares(f);
     }
-    sum = wave_sum(sum);
-    const int wid = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) partial[wid] = sum;
+    for (uint32_t col = tail + t; col < n; col += T) sum = add_square(sum, Elem<X>::load(xr + col));
+    sum = warp32_sum(sum);
+    if ((t & 31) == 0) warp_sums[t >> 5] = sum;
     __syncthreads();
-    const int nw = blockDim.x >> 6;
-    float total = (threadIdx.x & 63) < nw ? partial[threadIdx.x & 63] : 0.0f;
-    total = wave_sum(total);
-    const float rstd = row_rstd<X, M>(total, inv_n, eps);
-    if (threadIdx.x == 0) rstd_out[row] = rstd;
-    for (uint32_t c = threadIdx.x; c < n; c += blockDim.x) {
-        const float w = AFFINE ? Elem<W>::load(weight + c) : 0.0f;
-        Elem<X>::store(yr + c, normalize<X, W, M, AFFINE>(Elem<X>::load(xr + c), w, rstd, offset));
+    float p[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) p[i] = warp_sums[i];
+    const float rstd = row_rstd<X, M>(warp_tree<NW>(p), inv_n, eps);
+    if (t == 0) rstd_out[row] = rstd;
+    for (uint32_t col = 8 * t; col < tail; col += 8 * T) {
+        float f[8], w[8], o[8];
+        load_group<X>(xr + col, f);
+        if constexpr (AFFINE) load_group<W>(weight + col, w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            o[e] = normalize<X, W, M, AFFINE>(f[e], AFFINE ? w[e] : 0.0f, rstd, offset);
+        store_group<X>(yr + col, o);
+    }
+    for (uint32_t col = tail + t; col < n; col += T) {
+        const float w = AFFINE ? Elem<W>::load(weight + col) : 0.0f;
+        store_rn<X>(yr + col, normalize<X, W, M, AFFINE>(Elem<X>::load(xr + col), w, rstd, offset));
     }
 }
 
@@ -249,7 +398,7 @@ __global__ void __launch_bounds__(1024) rms_bwd_block(X* dx, float* __restrict__
             const float xv = Elem<X>::load(x + base + c);
             float g = g0;
             if constexpr (AFFINE) g *= Elem<W>::load(weight + c) + offset;
-            Elem<X>::store(dx + base + c, r * g + r * (correction * xv));
+            store_rn<X>(dx + base + c, r * g + r * (correction * xv));
             if constexpr (AFFINE) {
                 const bool rw = Casting<M>::round_weight_grad;
                 const float x_hat = rw ? rnd<X>(xv * r) : xv * r;
@@ -421,7 +570,7 @@ __global__ void __launch_bounds__(64 * kReduceWaves) reduce_weight_grad(W* __res
         float total = 0.0f;
 #pragma unroll
         for (int w = 0; w < kReduceWaves; ++w) total += run_sum[w][lane];
-        Elem<W>::store(dw + c, total);
+        store_rn<W>(dw + c, total);
     }
 }
 
@@ -493,8 +642,8 @@ void check_contiguous(const kcr_tensor* t, const char* name) {
     require_device(t, name);
 }
 
-// Threads per block for rows of n elements (warp counts of ops.rs:98-106,
-// expressed in 64-lane waves).
+// Threads per block of the reference for rows of n elements (ops.rs:98-106);
+// the forward kernels reproduce its reduction order for this count.
 unsigned block_threads(int64_t n) {
     if (n < 2048) return 128;
     if (n < 8192) return 256;
@@ -509,8 +658,8 @@ struct Fwd {
     hipStream_t stream;
 };
 
-template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
-void launch_wave(const Fwd& f, uint32_t nvec) {
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS, int SLOTS>
+void launch_wave(const Fwd& f, uint32_t groups) {
     const uint64_t waves_needed = static_cast<uint64_t>(f.rows);
     uint64_t blocks = (waves_needed + kWaves - 1) / kWaves;
     // Six blocks (24 waves) per CU, each wave looping over rows with one row
@@ -518,31 +667,55 @@ void launch_wave(const Fwd& f, uint32_t nvec) {
     // wave per row vs 45.5 us for this shape.
     const uint64_t cap = 6ull * compute_units();
     if (blocks > cap) blocks = cap;
-    rms_fwd_wave<X, W, M, AFFINE, CHUNKS><<<static_cast<unsigned>(blocks), 64 * kWaves, 0, f.stream>>>(
-        static_cast<u32x4*>(f.y->data), static_cast<float*>(f.rstd->data),
-        static_cast<const u32x4*>(f.x->data),
-        static_cast<const u32x4*>(AFFINE ? f.w->data : f.x->data), static_cast<uint32_t>(f.rows),
-        nvec, 1.0f / static_cast<float>(f.n), f.eps, f.offset);
+    rms_fwd_wave<X, W, M, AFFINE, CHUNKS, SLOTS><<<static_cast<unsigned>(blocks), 64 * kWaves, 0, f.stream>>>(
+        static_cast<X*>(f.y->data), static_cast<float*>(f.rstd->data),
+        static_cast<const X*>(f.x->data),
+        static_cast<const W*>(AFFINE ? f.w->data : f.x->data), static_cast<uint32_t>(f.rows),
+        groups, 1.0f / static_cast<float>(f.n), f.eps, f.offset);
+}
+
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS>
+void launch_wave_slots(const Fwd& f, uint32_t groups) {
+    switch (block_threads(f.n)) {
+        case 128: return launch_wave<X, W, M, AFFINE, CHUNKS, 2>(f, groups);
+        case 256: return launch_wave<X, W, M, AFFINE, CHUNKS, 4>(f, groups);
+        default: return launch_wave<X, W, M, AFFINE, CHUNKS, 8>(f, groups);
+    }
 }
 
 template <typename X, typename W, int M, bool AFFINE>
 void launch_fwd(const Fwd& f) {
-    constexpr int VEC = vec_of<X>();
-    const bool aligned = aligned16(f.x->data) && aligned16(f.y->data) &&
-                         (!AFFINE || aligned16(f.w->data));
-    if (aligned && f.n % VEC == 0) {
-        const uint32_t nvec = static_cast<uint32_t>(f.n / VEC);
-        const uint32_t chunks = (nvec + 63) / 64;
-        if (chunks <= 1) return launch_wave<X, W, M, AFFINE, 1>(f, nvec);
-        if (chunks <= 2) return launch_wave<X, W, M, AFFINE, 2>(f, nvec);
-        if (chunks <= 4) return launch_wave<X, W, M, AFFINE, 4>(f, nvec);
-        if (chunks <= 8) return launch_wave<X, W, M, AFFINE, 8>(f, nvec);
-        if (chunks <= 16) return launch_wave<X, W, M, AFFINE, 16>(f, nvec);
+    // The reference's 16-byte condition (ops.rs:108-115): rows of a multiple
+    // of 16 bytes and 16-byte aligned x, y and weight.
+    const bool vectorized = (f.n * sizeof(typename Elem<X>::storage)) % 16 == 0 &&
+                            aligned16(f.x->data) && aligned16(f.y->data) &&
+                            (!AFFINE || aligned16(f.w->data));
+    // Registers hold at most 16 x 16 bytes of the row per lane (8192 16-bit or
+    // 4096 f32 columns); the slot count T / 64 is at most 8 there.
+    constexpr int kMaxChunks = sizeof(typename Elem<X>::storage) == 4 ? 8 : 16;
+    if (vectorized && f.n % 8 == 0 && f.n <= 64 * 8 * kMaxChunks) {
+        const uint32_t groups = static_cast<uint32_t>(f.n / 8);
+        const uint32_t chunks = (groups + 63) / 64;
+        if (chunks <= 1) return launch_wave_slots<X, W, M, AFFINE, 1>(f, groups);
+        if (chunks <= 2) return launch_wave_slots<X, W, M, AFFINE, 2>(f, groups);
+        if (chunks <= 4) return launch_wave_slots<X, W, M, AFFINE, 4>(f, groups);
+        if (chunks <= 8) return launch_wave_slots<X, W, M, AFFINE, 8>(f, groups);
+        if constexpr (kMaxChunks == 16) return launch_wave_slots<X, W, M, AFFINE, 16>(f, groups);
     }
-    rms_fwd_block<X, W, M, AFFINE><<<static_cast<unsigned>(f.rows), block_threads(f.n), 0, f.stream>>>(
-        static_cast<X*>(f.y->data), static_cast<float*>(f.rstd->data),
-        static_cast<const X*>(f.x->data), static_cast<const W*>(AFFINE ? f.w->data : f.x->data),
-        static_cast<uint32_t>(f.n), 1.0f / static_cast<float>(f.n), f.eps, f.offset);
+    auto go = [&](auto nw_tag) {
+        constexpr int NW = decltype(nw_tag)::value;
+        rms_fwd_block<X, W, M, AFFINE, NW><<<static_cast<unsigned>(f.rows), 32 * NW, 0, f.stream>>>(
+            static_cast<X*>(f.y->data), static_cast<float*>(f.rstd->data),
+            static_cast<const X*>(f.x->data), static_cast<const W*>(AFFINE ? f.w->data : f.x->data),
+            static_cast<uint32_t>(f.n), vectorized ? 1u : 0u, 1.0f / static_cast<float>(f.n), f.eps,
+            f.offset);
+    };
+    switch (block_threads(f.n)) {
+        case 128: return go(std::integral_constant<int, 4>{});
+        case 256: return go(std::integral_constant<int, 8>{});
+        case 512: return go(std::integral_constant<int, 16>{});
+        default: return go(std::integral_constant<int, 32>{});
+    }
 }
 
 // Dispatch over (mode, X, W, AFFINE) like ops.rs:136-184; `L` is a functor

@@ -48,6 +48,34 @@ def _erf(x):
     return _erf64(np.asarray(x, dtype=np.float64)).astype(F32)
 
 
+def fma32(a, b, c) -> np.ndarray:
+    """Correctly rounded f32 a*b + c (one rounding), for f32 arrays.
+
+    a*b is exact in f64; the f64 sum s = a*b + c is rounded, and TwoSum gives
+    its exact error e. Rounding s to f32 is then correct except when s lies
+    exactly halfway between two floats and e != 0, where the tie is broken
+    toward the side of e (no other f64 value can sit between the exact sum and
+    s across an f32 midpoint, as every such midpoint is an f64 number).
+    """
+    a64 = np.asarray(a, dtype=np.float32).astype(np.float64)
+    b64 = np.asarray(b, dtype=np.float32).astype(np.float64)
+    c64 = np.asarray(c, dtype=np.float32).astype(np.float64)
+    p = a64 * b64
+    with np.errstate(over="ignore", invalid="ignore"):
+        s = p + c64
+        bb = s - p
+        e = (p - (s - bb)) + (c64 - bb)
+        r = s.astype(F32)
+        up = np.nextafter(r, np.float32(np.inf))
+        down = np.nextafter(r, np.float32(-np.inf))
+        other = np.where(s > r.astype(np.float64), up, down)
+        tie = (np.isfinite(s) & np.isfinite(e) & (e != 0)
+               & ((r.astype(np.float64) + other.astype(np.float64)) * 0.5 == s))
+        # at a tie the exact sum lies on the side of e: pick the float on that side
+        toward = np.where(e > 0, np.maximum(r, other), np.minimum(r, other))
+    return np.where(tie, toward, r).astype(F32)
+
+
 def act(name: str, x, dtype: str, threshold: float = 0.0) -> np.ndarray:
     """act(x) rounded to `dtype`, for x holding values of that dtype."""
     R = rounder(dtype)
@@ -63,7 +91,7 @@ def act(name: str, x, dtype: str, threshold: float = 0.0) -> np.ndarray:
             kappa = F32(0.044715)
             x_cube = f * f * f
             # fused multiply-add: one rounding of kappa * x^3 + f
-            inner = beta * (kappa.astype(np.float64) * x_cube.astype(np.float64) + f).astype(F32)
+            inner = beta * fma32(np.broadcast_to(kappa, np.shape(f)), x_cube, f)
             return R(F32(0.5) * f * (F32(1.0) + _tanh(inner)))
         if name == "gelu_new":  # activation.rs:79-90
             x3 = R(R(f * f) * f)

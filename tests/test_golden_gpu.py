@@ -4,10 +4,9 @@ through the same Python ops a caller of the reference uses.
 Bars (the north star's and the reference tests'): attention output max-abs
 <= 2e-2 against the fp32 oracle; gradients at the reference's bf16 backward
 tolerance (atol 0.06, rtol 0.08, flash-attn2-rs/tests/test_gold.py:267);
-RMSNorm within 2 bf16 ulp with under 0.1 % of elements beyond 1 ulp
-(llama casting: the summation order of mean(x^2) can move x_hat by one ulp
-before the weight product rounds); gated activations within the rounded
-act's ulp times |up| plus one ulp of the result.
+RMSNorm and the gated activations bit for bit (the kernels sum mean(x^2) in
+the reference's order and round rstd correctly; 16-bit activations come from
+exact tables and the product is rounded once).
 """
 
 import sys
@@ -17,7 +16,6 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import activation as A
 from oracle.numerics import ulp_distance_bf16
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -74,9 +72,9 @@ def test_golden_rms_norm():
     y = torch.empty_like(x)
     rstd = torch.empty(x.shape[0], device="cuda")
     rmsnorm.ops.rms_norm_forward(y, rstd, x, w, G.RMS["eps"], 0.0, "llama")
-    dist = ulp_distance_bf16(y.float().cpu().numpy(), G.from_bits(d["y"]))
-    assert dist.max() <= 2 and (dist > 1).mean() < 1e-3
-    np.testing.assert_allclose(rstd.cpu().numpy(), d["rstd"], rtol=2e-6)
+    assert np.array_equal(y.float().cpu().numpy().view(np.uint32),
+                          G.from_bits(d["y"]).view(np.uint32))
+    assert np.array_equal(rstd.cpu().numpy().view(np.uint32), d["rstd"].view(np.uint32))
 
 
 @pytest.mark.parametrize("op", ["silu_and_mul", "gelu_and_mul", "gelu_tanh_and_mul"])
@@ -89,16 +87,4 @@ def test_golden_gated(op):
     getattr(activation_rs.ops, op)(out, x)
     got = out.float().cpu().numpy()
     exp = G.from_bits(d[op])
-    xn = G.from_bits(d["x"])
-    h = xn.shape[1] // 2
-    gate, up = xn[:, :h], xn[:, h:]
-    act = A.act(A.GATED[op][0], gate, "bf16")
-
-    def ulp(a):
-        return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(a), 2.0**-126))) - 7)
-
-    bound = ulp(act) * np.abs(up) + ulp(exp)
-    if op != "silu_and_mul":
-        bound += np.abs(gate) * np.abs(up) * 2.0**-23  # 1 + erf / 1 + tanh cancellation
-    assert np.all(np.abs(got - exp) <= bound)
-    assert (ulp_distance_bf16(got, exp) > 1).mean() < 1e-3
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), ulp_distance_bf16(got, exp).max()

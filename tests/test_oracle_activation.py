@@ -128,3 +128,42 @@ def test_gelu_new_fast_vs_reference_test_formula(name, fn, dtype):
     # and a dropped cubic term would not pass:
     wrong = 0.5 * x * (1.0 + torch.tanh(0.7978845608 * x))
     assert not torch.allclose(ours.float(), wrong.float(), atol=atol, rtol=rtol)
+
+
+def test_fma32_against_exact_rationals():
+    """oracle.activation.fma32 equals the correctly rounded a*b + c computed with
+    exact rationals, on random triples and on constructed halfway cases where a
+    plain f64 evaluation rounds twice."""
+    from fractions import Fraction
+
+    from oracle.activation import fma32
+
+    def exact(a, b, c):
+        v = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+        lo = np.float32(float(v))  # nearest f64 then f32: candidate neighbourhood
+        cands = [np.nextafter(lo, np.float32(-np.inf)), lo, np.nextafter(lo, np.float32(np.inf))]
+        best = min(cands, key=lambda r: (abs(Fraction(float(r)) - v),
+                                         int(np.float32(r).view(np.uint32)) & 1))
+        return np.float32(best)
+
+    g = np.random.default_rng(0)
+    a = g.standard_normal(3000).astype(np.float32)
+    b = (g.standard_normal(3000) * 10).astype(np.float32)
+    c = g.standard_normal(3000).astype(np.float32)
+    # halfway cases: c = 1 + 2^-24 (an f32 midpoint offset) with a tiny product
+    a2 = np.full(8, 2.0**-30, np.float32)
+    b2 = np.array([2.0**-40, -(2.0**-40), 2.0**-50, -(2.0**-50), 1e-20, -1e-20, 2.0**-60, -(2.0**-60)], np.float32)
+    c2 = np.full(8, 1.0 + 2.0**-23, np.float32)
+    # p = (1 + 2^-23) * 2^-24 (1 - 2^-23) = 2^-24 - 2^-70: p + c is just below
+    # (or, negated, above) an f32 midpoint and a plain f64 sum lands on it
+    u = 2.0**-23
+    a3 = np.array([1 + u, 1 + u, -(1 + u), 1 + u], np.float32)
+    b3 = np.array([2.0**-24 * (1 - u), 2.0**-24 * (1 - u), 2.0**-24 * (1 - u), 2.0**-25 * (1 - u)], np.float32)
+    c3 = np.array([1 + u, 1.0, -(1 + u), 0.5 + u / 2], np.float32)
+    A, B, C = (np.concatenate(t) for t in ((a, a2, a3), (b, b2, b3), (c, c2, c3)))
+    got = fma32(A, B, C)
+    want = np.array([exact(x, y, z) for x, y, z in zip(A, B, C)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a plain f64 evaluation rounds twice on at least one of the constructed cases
+    naive = (A.astype(np.float64) * B + C).astype(np.float32)
+    assert not np.array_equal(naive.view(np.uint32), want.view(np.uint32))

@@ -94,3 +94,62 @@ def test_backward_vs_torch_autograd(mode, offset, affine):
     np.testing.assert_allclose(dx, xg.grad.numpy(), rtol=1e-4, atol=1e-5)
     if affine:
         np.testing.assert_allclose(dw, wg.grad.numpy(), rtol=1e-4, atol=1e-4)
+
+
+def _literal_block_sum(row, vectorized):
+    """Thread-by-thread restatement of the reference kernel's sum of squares
+    (rmsnorm/src/device.rs:41-63, 113-145): a literal loop per thread, then
+    shuffle-xor butterflies over explicit 32-lane arrays, all in f32."""
+    f = np.float32
+    n = len(row)
+    T = R.block_threads(n)
+    tail = n // 8 * 8 if vectorized else 0
+    partial = []
+    for t in range(T):
+        s = f(0.0)
+        col = 8 * t
+        first = True
+        while col < tail:
+            g = f(0.0)
+            for i in range(8):
+                g = f(g + f(row[col + i] * row[col + i]))
+            s = g if first else f(s + g)
+            first = False
+            col += 8 * T
+        col = tail + t
+        while col < n:
+            s = f(s + f(row[col] * row[col]))
+            col += T
+        partial.append(s)
+
+    def warp_reduce(lanes):
+        lanes = list(lanes)
+        for d in (16, 8, 4, 2, 1):
+            lanes = [f(lanes[i] + lanes[i ^ d]) for i in range(32)]
+        assert len(set(np.asarray(lanes).view(np.uint32).tolist())) == 1  # every lane agrees
+        return lanes[0]
+
+    warps = [warp_reduce(partial[32 * w : 32 * w + 32]) for w in range(T // 32)]
+    return warp_reduce(warps + [f(0.0)] * (32 - len(warps)))
+
+
+@pytest.mark.parametrize("n,vectorized", [(96, True), (1000, True), (1001, False), (4096, True),
+                                          (2052, True), (300, False), (8200, True)])
+def test_sum_order_matches_literal_thread_loop(n, vectorized):
+    g = np.random.default_rng(n)
+    x = g.standard_normal((3, n)).astype(np.float32)
+    got = R.sum_squares_reference_order(x, vectorized)
+    want = np.array([_literal_block_sum(r, vectorized) for r in x], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # and it is a sum of squares to f32 accuracy
+    np.testing.assert_allclose(got, (x.astype(np.float64) ** 2).sum(-1), rtol=n * 2.0**-24)
+
+
+def test_rsqrt_is_correctly_rounded():
+    g = np.random.default_rng(0)
+    v = np.concatenate([g.uniform(1e-6, 10, 20000), [1.0, 4.0, 0.25, 1e-6, 2.0]]).astype(np.float32)
+    r = R.rsqrt_rn(v)
+    exact = 1.0 / np.sqrt(v.astype(np.longdouble))
+    err = np.abs(r.astype(np.longdouble) - exact) / np.spacing(r).astype(np.longdouble)
+    assert err.max() <= 0.5 + 1e-6
+    assert r[-5:].tolist() == [1.0, 0.5, 2.0, np.float32(1000.0), np.float32(1 / np.sqrt(2.0))]
