@@ -206,6 +206,26 @@ int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const k
                           int64_t workspace_bytes, const kcr_tensor* out, const kcr_tensor* lse,
                           void* stream);
 
+/* Attention over a KV cache without allocation: kcr_flash_fwd_kvcache with the
+ * split partials in a fixed scratch array inside the library instead of a
+ * caller workspace. No counterpart in the reference; it is for callers that
+ * cannot allocate (code under HIP graph capture, tight decode loops, harnesses
+ * that forbid hipMalloc). Each GPU holds one scratch array of
+ * kcr_flash_fwd_kvcache_noalloc_scratch_bytes() bytes (64 MiB) for the life of
+ * the process, shared by every call on that GPU: calls that overlap on one GPU
+ * (concurrent streams) race on it. A call whose num_splits x heads x total_q x
+ * (head_dim + 1) x 4 bytes exceed it fails with KCR_VALUE_ERROR. num_splits <= 1
+ * uses no scratch. No hipMalloc, hipFree or allocating library call is made;
+ * the first call on a device looks up the scratch address there. */
+int64_t kcr_flash_fwd_kvcache_noalloc_scratch_bytes(void);
+int kcr_flash_fwd_kvcache_noalloc(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
+                                  const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k, int64_t new_keys,
+                                  const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                                  const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
+                                  double scale, int causal, int64_t window_left, int64_t window_right,
+                                  double softcap, int64_t max_seqlen_q, int64_t num_splits,
+                                  const kcr_tensor* out, const kcr_tensor* lse, void* stream);
+
 /* Backward preprocess. replaces `bwd_preprocess(dout, out, p)`
  * (flash-attn2-rs/src/host/backward.rs:628-737):
  *   delta[b,h,s] = sum_d dout*out * (1-p), float32 [B,H,round128(Sq)], rows >= Sq are 0. */

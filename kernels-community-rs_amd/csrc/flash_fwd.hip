@@ -32,6 +32,9 @@
 
 #include "attention.h"
 
+#include <mutex>
+#include <vector>
+
 namespace kcr {
 namespace attn {
 
@@ -1549,15 +1552,19 @@ extern "C" int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int
     return num_splits * heads * total_q * (d + 1) * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
-                                     const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k,
-                                     int64_t new_keys, const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
-                                     const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
-                                     double scale, int causal, int64_t window_left, int64_t window_right,
-                                     double softcap, int64_t max_seqlen_q, int64_t num_splits, void* workspace,
-                                     int64_t workspace_bytes, const kcr_tensor* out, const kcr_tensor* lse,
-                                     void* stream) {
-    return guarded([&] {
+namespace {
+
+// The cached-attention launch behind both kvcache entry points. `workspace`
+// holds the split partials; `noalloc` names the fixed scratch of the
+// allocation-free entry point in the size error.
+void fwd_kvcache_impl(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
+                      const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k, int64_t new_keys,
+                      const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                      const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale, double scale,
+                      int causal, int64_t window_left, int64_t window_right, double softcap,
+                      int64_t max_seqlen_q, int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                      bool noalloc, const kcr_tensor* out, const kcr_tensor* lse, void* stream) {
+    {
         // Batched form: q/out [B, R, H, D] (any strides) and lse [B, H, R], no cu_seqlens_q.
         const bool batched = q && q->ndim == 4 && !cu_seqlens_q;
         check_qkv(q, "q", batched ? 4 : 3);
@@ -1702,6 +1709,13 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
         const int64_t splits = tiled ? std::max<int64_t>(1, num_splits) : 1;
         if (splits > 1) {
             const int64_t need = kcr_flash_fwd_kvcache_workspace_bytes(splits, H, Tq, D);
+            if (noalloc && need > workspace_bytes) {
+                throw value_error(std::to_string(splits) + " splits over " + std::to_string(H) + " heads x " +
+                                  std::to_string(Tq) + " query rows need " + std::to_string(need) +
+                                  " bytes of split scratch; kcr_flash_fwd_kvcache_noalloc holds at most " +
+                                  std::to_string(workspace_bytes) +
+                                  " (use fewer splits, or kcr_flash_fwd_kvcache with a workspace)");
+            }
             if (!workspace || workspace_bytes < need) {
                 throw value_error("workspace must hold " + std::to_string(need) + " bytes for " +
                                   std::to_string(splits) + " splits");
@@ -1737,5 +1751,64 @@ extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcac
             }
             check_launch("launch merge_splits");
         }
+    }
+}
+
+// Split scratch of the allocation-free entry point: one copy per GPU, resident
+// until the process ends. Host code reaches it only through the per-device
+// address from hipGetSymbolAddress (the array's name is a host-side stand-in).
+constexpr int64_t kNoAllocScratchBytes = 64ll << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+void* noalloc_scratch() {
+    static std::mutex mu;
+    static std::vector<void*> addr;
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    if (static_cast<size_t>(device) >= addr.size()) addr.resize(device + 1, nullptr);
+    if (!addr[device]) {
+        void* p = nullptr;
+        check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        addr[device] = p;
+    }
+    return addr[device];
+}
+
+}  // namespace
+
+extern "C" int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,
+                                     const kcr_tensor* cu_seqlens_q, const kcr_tensor* seqused_k,
+                                     int64_t new_keys, const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                                     const kcr_tensor* block_table, const kcr_tensor* alibi, int has_scale,
+                                     double scale, int causal, int64_t window_left, int64_t window_right,
+                                     double softcap, int64_t max_seqlen_q, int64_t num_splits, void* workspace,
+                                     int64_t workspace_bytes, const kcr_tensor* out, const kcr_tensor* lse,
+                                     void* stream) {
+    return guarded([&] {
+        fwd_kvcache_impl(q, kcache, vcache, cu_seqlens_q, seqused_k, new_keys, leftpad_k, cache_batch_idx,
+                         block_table, alibi, has_scale, scale, causal, window_left, window_right, softcap,
+                         max_seqlen_q, num_splits, workspace, workspace_bytes, false, out, lse, stream);
+    });
+}
+
+extern "C" int64_t kcr_flash_fwd_kvcache_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int kcr_flash_fwd_kvcache_noalloc(const kcr_tensor* q, const kcr_tensor* kcache,
+                                             const kcr_tensor* vcache, const kcr_tensor* cu_seqlens_q,
+                                             const kcr_tensor* seqused_k, int64_t new_keys,
+                                             const kcr_tensor* leftpad_k, const kcr_tensor* cache_batch_idx,
+                                             const kcr_tensor* block_table, const kcr_tensor* alibi,
+                                             int has_scale, double scale, int causal, int64_t window_left,
+                                             int64_t window_right, double softcap, int64_t max_seqlen_q,
+                                             int64_t num_splits, const kcr_tensor* out, const kcr_tensor* lse,
+                                             void* stream) {
+    return guarded([&] {
+        void* ws = num_splits > 1 ? noalloc_scratch() : nullptr;
+        fwd_kvcache_impl(q, kcache, vcache, cu_seqlens_q, seqused_k, new_keys, leftpad_k, cache_batch_idx,
+                         block_table, alibi, has_scale, scale, causal, window_left, window_right, softcap,
+                         max_seqlen_q, num_splits, ws, ws ? kNoAllocScratchBytes : 0, true, out, lse, stream);
     });
 }
