@@ -192,3 +192,48 @@ def test_baseline_config_backward_subset():
     np.testing.assert_allclose(dq[b:b + 1, :, sl].float().cpu().numpy(), edq, atol=0.06, rtol=0.08)
     np.testing.assert_allclose(dk[b:b + 1, :, grp:grp + 1].float().cpu().numpy(), edk, atol=0.06, rtol=0.08)
     np.testing.assert_allclose(dv[b:b + 1, :, grp:grp + 1].float().cpu().numpy(), edv, atol=0.06, rtol=0.08)
+
+
+def test_varlen_baseline_config_backward():
+    """BASELINE config 5 backward: 16 sequences with lengths ~U[128, 8192] (seed 5),
+    Hq=32, Hkv=8, D=128, causal bf16, dO ~N(0,1): the whole varlen_fwd +
+    varlen_bwd launch; dQ of query heads 8-11 and dK/dV of their KV head 2
+    (the complete GQA sum of that group) for sequences 0, 7 and 15 against the
+    oracle's gradients, at the reference's bf16 backward tolerance
+    (test_gold.py:267), and the delta rows of those sequences."""
+    import flash_attn2_rs
+
+    lens = torch.randint(128, 8193, (16,), generator=torch.Generator().manual_seed(5)).tolist()
+    cu = torch.tensor(np.cumsum([0] + lens), dtype=torch.int32)
+    total = int(cu[-1])
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(total, 32, 128, generator=g).bfloat16()
+    k = torch.randn(total, 8, 128, generator=g).bfloat16()
+    v = torch.randn(total, 8, 128, generator=g).bfloat16()
+    dout = torch.randn(total, 32, 128, generator=g).bfloat16()
+    ops = flash_attn2_rs.ops
+    qd, kd, vd, dod, cud = q.cuda(), k.cuda(), v.cuda(), dout.cuda(), cu.cuda()
+    mx = max(lens)
+    out, lse, _ = ops.varlen_fwd_explicit(qd, kd, vd, cud, cud, None, None, None, None, True, -1, -1,
+                                          0.0, 0.0, None, mx, mx, False, False)
+    dq, dk, dv, delta = ops.varlen_bwd_explicit(qd, kd, vd, dod, out, lse, cud, cud, None, None, True,
+                                                -1, -1, 0.0, 0.0, None, mx, mx, False)
+    for t in (dq, dk, dv):
+        assert torch.isfinite(t).all()
+    hs, grp = slice(8, 12), 2
+    for s in (0, 7, 15):
+        a, b = int(cu[s]), int(cu[s + 1])
+        edq, edk, edv, edelta = OA.backward(
+            q[None, a:b, hs].float().numpy(), k[None, a:b, grp:grp + 1].float().numpy(),
+            v[None, a:b, grp:grp + 1].float().numpy(), out[a:b, hs][None].float().cpu().numpy(),
+            dout[None, a:b, hs].float().numpy(), lse[hs, a:b][None].cpu().numpy(), causal=True)
+        np.testing.assert_allclose(dq[a:b, hs].float().cpu().numpy(), edq[0], atol=0.06, rtol=0.08)
+        np.testing.assert_allclose(dk[a:b, grp].float().cpu().numpy(), edk[0, :, 0], atol=0.06, rtol=0.08)
+        np.testing.assert_allclose(dv[a:b, grp].float().cpu().numpy(), edv[0, :, 0], atol=0.06, rtol=0.08)
+        # delta [H, Tq + 128 B]: row qs + 128 b of sequence b (host/varlen/backward.rs:173-178)
+        np.testing.assert_allclose(delta[hs, a + 128 * s:b + 128 * s].cpu().numpy(), edelta[0],
+                                   atol=2e-3, rtol=2e-4)
+        print(f"config 5 seq {s} (L={b - a}): max |dq err| "
+              f"{np.abs(dq[a:b, hs].float().cpu().numpy() - edq[0]).max():.3g}, "
+              f"|dk err| {np.abs(dk[a:b, grp].float().cpu().numpy() - edk[0, :, 0]).max():.3g}, "
+              f"|dv err| {np.abs(dv[a:b, grp].float().cpu().numpy() - edv[0, :, 0]).max():.3g}")
