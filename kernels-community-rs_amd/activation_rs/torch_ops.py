@@ -1,45 +1,47 @@
-"""The activation ops registered as torch custom ops (for `torch.compile` and
-`torch.library.opcheck`), mirroring activation-rs/tvm-ffi-ext/activation_rs/
-torch_ops.py:10-45: every op mutates `out` and returns nothing."""
+"""torch.library registration of the activation ops, in the namespace
+`kcr_activation`, for `torch.compile` and `torch.library.opcheck`.
+
+Interface kept from the reference (activation-rs/tvm-ffi-ext/activation_rs/
+torch_ops.py): the eleven op names, `(out, input)` arguments (plus `threshold`
+for fatrelu_and_mul), that each op writes `out` and returns nothing. Here the
+ops come from one table of names and schemas, declared on a
+`torch.library.Library` with a CUDA entry that calls the C ABI shim and a fake
+entry with no outputs.
+"""
+
+from __future__ import annotations
 
 import torch
 
-from ._ops import ops
-from ._ops import torch_add_op_namespace_prefix as add_op_namespace_prefix
+from ._ops import ops, torch_add_op_namespace_prefix
+
+NAMESPACE = torch_add_op_namespace_prefix("silu").split("::")[0]
+_lib = torch.library.Library(NAMESPACE, "DEF")
+
+_UNARY = "(Tensor(a!) out, Tensor input) -> ()"
+_SCHEMAS = {
+    "silu_and_mul": _UNARY,
+    "mul_and_silu": _UNARY,
+    "gelu_and_mul": _UNARY,
+    "gelu_tanh_and_mul": _UNARY,
+    "fatrelu_and_mul": "(Tensor(a!) out, Tensor input, float threshold) -> ()",
+    "gelu_new": _UNARY,
+    "gelu_fast": _UNARY,
+    "gelu_quick": _UNARY,
+    "gelu_tanh": _UNARY,
+    "silu": _UNARY,
+    "gelu": _UNARY,
+}
 
 
-def _register(name: str, impl):
-    op = torch.library.custom_op(
-        add_op_namespace_prefix(name),
-        impl,
-        mutates_args=("out",),
-        device_types="cuda",
-    )
-    op.register_fake(lambda *args: None)
-    return op
+def _no_outputs(*args):
+    return None
 
 
-def _activation_op(name: str):
-    native = getattr(ops, name)
+for _name, _schema in _SCHEMAS.items():
+    _lib.define(_name + _schema)
+    _lib.impl(_name, getattr(ops, _name), "CUDA")
+    torch.library.register_fake(f"{NAMESPACE}::{_name}", _no_outputs, lib=_lib)
+    globals()[_name] = getattr(getattr(torch.ops, NAMESPACE), _name).default
 
-    def impl(out: torch.Tensor, input: torch.Tensor) -> None:
-        native(out, input)
-
-    return _register(name, impl)
-
-
-def _fatrelu_and_mul(out: torch.Tensor, input: torch.Tensor, threshold: float) -> None:
-    ops.fatrelu_and_mul(out, input, threshold)
-
-
-silu_and_mul = _activation_op("silu_and_mul")
-mul_and_silu = _activation_op("mul_and_silu")
-gelu_and_mul = _activation_op("gelu_and_mul")
-gelu_tanh_and_mul = _activation_op("gelu_tanh_and_mul")
-fatrelu_and_mul = _register("fatrelu_and_mul", _fatrelu_and_mul)
-gelu_new = _activation_op("gelu_new")
-gelu_fast = _activation_op("gelu_fast")
-gelu_quick = _activation_op("gelu_quick")
-gelu_tanh = _activation_op("gelu_tanh")
-silu = _activation_op("silu")
-gelu = _activation_op("gelu")
+__all__ = sorted(_SCHEMAS)

@@ -5,6 +5,8 @@
 
 #include "common.h"
 
+#include <initializer_list>
+
 namespace kcr {
 namespace attn {
 
@@ -620,6 +622,47 @@ __device__ __forceinline__ uint32_t keep_bits_key_lane_shared(const DropoutState
     }
     return bits;
 }
+
+// ---------------------------------------------------------------------------
+// Layout staging (layout.hip): what prepare_attention_tensor and the `out`
+// copy of flash-attn2-rs/src/host/layout.rs:46-125 and host/forward/mod.rs:
+// 349-376 do. An attention tensor whose rows the kernels cannot read as
+// 16-byte vectors (base not 16-byte aligned, an outer stride not a multiple
+// of 8 elements) or, for K/V, whose sequence rows overlap or are more than
+// 2^23 elements apart, is copied into a packed buffer first; an output with
+// such rows, or one overlapping an input, is written to a packed buffer and
+// copied out afterwards. Buffers come from the stream-ordered allocator
+// (hipMallocAsync / hipFreeAsync on the call's stream), as the reference takes
+// them from its caller's allocator.
+// ---------------------------------------------------------------------------
+class Staged {
+public:
+    // `seq_dim` >= 0 adds the K/V sequence-row checks for that dimension
+    // (head size `d`). With copy_in the tensor's values are copied into the
+    // packed buffer (inputs); without, only the buffer is made (outputs).
+    Staged(const kcr_tensor* t, hipStream_t s, bool copy_in, int seq_dim = -1, int64_t d = 0,
+           std::initializer_list<const kcr_tensor*> must_not_overlap = {});
+    ~Staged();
+    Staged(const Staged&) = delete;
+    Staged& operator=(const Staged&) = delete;
+    const kcr_tensor* get() const { return buffer_ ? &packed_ : src_; }
+    bool staged() const { return buffer_ != nullptr; }
+    // Copies the packed buffer back into the caller's tensor (outputs).
+    void copy_out();
+
+private:
+    const kcr_tensor* src_;
+    kcr_tensor packed_{};
+    void* buffer_ = nullptr;
+    hipStream_t stream_;
+};
+
+// Whether two tensors' byte ranges intersect.
+bool spans_overlap(const kcr_tensor* a, const kcr_tensor* b);
+
+// Whether no two elements of `t` share an address (strides non-negative and,
+// taken in increasing order, each at least the span of the dimensions below).
+bool nonoverlapping_layout(const kcr_tensor* t);
 
 }  // namespace attn
 }  // namespace kcr

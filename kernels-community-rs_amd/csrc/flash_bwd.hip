@@ -1248,12 +1248,13 @@ extern "C" int kcr_flash_bwd_preprocess(const kcr_tensor* dout, const kcr_tensor
         }
         const int64_t rounded = (S + 127) / 128 * 128;
         check_f32_tensor(delta, {B, H, rounded}, "delta");
-        for (auto* t : {dout, out}) {
-            if (!rows_aligned16(t)) throw value_error("dout and out must have 16-byte aligned rows");
-            require_device(t, "dout/out");
-        }
+        for (auto* t : {dout, out}) require_device(t, "dout/out");
         if (S == 0) return;
         auto s = static_cast<hipStream_t>(stream);
+        // Packed copies of rows the kernel cannot read as 16-byte vectors (host/layout.rs:46-125).
+        Staged sd_(dout, s, true), so_(out, s, true);
+        dout = sd_.get();
+        out = so_.get();
         const int lanes = D <= 64 ? 8 : (D <= 128 ? 16 : 32);
         const int64_t rows = B * H * rounded;
         const int64_t blocks = rows / (256 / lanes);
@@ -1309,11 +1310,14 @@ extern "C" int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         check_grad(dq, q, "dq");
         check_grad(dk, k, "dk");
         check_grad(dv, v, "dv");
-        for (auto* t : {q, k, v, dout}) {
-            if (!rows_aligned16(t)) throw value_error("q, k, v and dout must have 16-byte aligned rows");
-            require_device(t, "q/k/v/dout");
-        }
+        for (auto* t : {q, k, v, dout}) require_device(t, "q/k/v/dout");
         auto s = static_cast<hipStream_t>(stream);
+        // Packed copies of inputs the tile loads cannot read (host/layout.rs:46-125).
+        Staged sq_(q, s, true), sk_(k, s, true, 1, D), sv_(v, s, true, 1, D), sd_(dout, s, true);
+        q = sq_.get();
+        k = sk_.get();
+        v = sv_.get();
+        dout = sd_.get();
         const double scale_used = has_scale ? scale : 1.0 / std::sqrt(static_cast<double>(D));
         const Options opt = normalize_options(has_scale, scale, causal, window_left, window_right, softcap, D, Sk);
         const DropoutArgs drop = parse_dropout(dropout, softcap, q);
@@ -1404,11 +1408,16 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
         check_grad(dq, q, "dq");
         check_grad(dk, k, "dk");
         check_grad(dv, v, "dv");
-        for (auto* t : {q, k, v, dout, out}) {
-            if (Tq > 0 && !rows_aligned16(t)) throw value_error("packed inputs must have 16-byte aligned rows");
-            require_device(t, "q/k/v/dout/out");
-        }
+        for (auto* t : {q, k, v, dout, out}) require_device(t, "q/k/v/dout/out");
         auto s = static_cast<hipStream_t>(stream);
+        // Packed copies of inputs the tile loads cannot read (host/layout.rs:46-125).
+        Staged sq_(q, s, true), sk_(k, s, true, 0, D), sv_(v, s, true, 0, D), sd_(dout, s, true),
+            so_(out, s, true);
+        q = sq_.get();
+        k = sk_.get();
+        v = sv_.get();
+        dout = sd_.get();
+        out = so_.get();
         const double scale_used = has_scale ? scale : 1.0 / std::sqrt(static_cast<double>(D));
         int causal_eff = causal;
         if (max_seqlen_q == 1 && !alibi) causal_eff = 0;

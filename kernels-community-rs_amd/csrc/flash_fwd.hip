@@ -1333,6 +1333,14 @@ void check_head_dim(int64_t d) {
 using namespace kcr;
 using namespace kcr::attn;
 
+namespace {
+// The dense forward launch over tensors the kernels accept as they are.
+void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* alibi,
+                   int32_t alibi_b, const Options& opt, const DropoutArgs& drop, int64_t B, int64_t Sq,
+                   int64_t H, int64_t D, int64_t Sk, int64_t Hk, const kcr_tensor* out,
+                   const kcr_tensor* lse, hipStream_t s);
+}  // namespace
+
 extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                              const kcr_tensor* alibi, int has_scale, double scale, int causal,
                              int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
@@ -1367,17 +1375,15 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         if (!out || shape_of(*out) != shape_of(*q) || out->dtype != q->dtype) {
             throw value_error("out must match q's shape, dtype and device");
         }
-        if (out->strides[3] != 1) throw value_error("out must have unit last stride");
+        if (out->strides[3] != 1 || !nonoverlapping_layout(out)) {
+            throw value_error("out must have unit last stride and nonoverlapping non-negative strides; unsupported "
+                              "writable layout: elements overlap or the bounded safety checks cannot prove they "
+                              "are disjoint. Use a separately allocated contiguous output.");
+        }
         if (!lse || lse->dtype != KCR_FLOAT32 || lse->ndim != 3 || lse->shape[0] != B ||
             lse->shape[1] != H || lse->shape[2] != Sq || !is_contiguous(*lse)) {
             throw value_error("lse must be contiguous float32 [B, H, Sq]");
         }
-        for (auto* t : {q, k, v, out}) {
-            if (!rows_aligned16(t)) {
-                throw value_error("q, k, v and out must have 16-byte aligned rows (strides multiple of 8 elements)");
-            }
-        }
-        check_kv_rows(k, v, 1, D);
         require_device(q, "q");
         require_device(k, "k");
         require_device(v, "v");
@@ -1388,6 +1394,27 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
                                               softcap, D, Sk);
         const DropoutArgs drop = parse_dropout(dropout, softcap, q);
         if (Sq == 0) return;
+        // Packed copies of inputs the tile loads cannot read, and of an output
+        // they cannot write or that overlaps an input (host/layout.rs:46-125,
+        // host/forward/mod.rs:349-376).
+        Staged sq_(q, s, true), sk_(k, s, true, 1, D), sv_(v, s, true, 1, D);
+        Staged so_(out, s, false, -1, 0, {q, k, v});
+        q = sq_.get();
+        k = sk_.get();
+        v = sv_.get();
+        out = so_.get();
+        run_dense_fwd(q, k, v, alibi, alibi_b, opt, drop, B, Sq, H, D, Sk, Hk, out, lse, s);
+        so_.copy_out();
+    });
+}
+
+namespace {
+
+void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* alibi,
+                   int32_t alibi_b, const Options& opt, const DropoutArgs& drop, int64_t B, int64_t Sq,
+                   int64_t H, int64_t D, int64_t Sk, int64_t Hk, const kcr_tensor* out,
+                   const kcr_tensor* lse, hipStream_t s) {
+    {
         if (Sk == 0) {
             // Every row is empty: O = 0, LSE = +inf.
             for (int64_t bi = 0; bi < B; ++bi) {
@@ -1429,8 +1456,10 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<false>(prm, q->dtype, bucket_for(D), general, s);
-    });
+    }
 }
+
+}  // namespace
 
 extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                                     const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
@@ -1481,12 +1510,6 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
             lse->shape[1] != Tq || !is_contiguous(*lse)) {
             throw value_error("lse must be contiguous float32 [H, total_q]");
         }
-        for (auto* t : {q, k, v, out}) {
-            if (Tq > 0 && !rows_aligned16(t)) {
-                throw value_error("q, k, v and out must have 16-byte aligned rows (strides multiple of 8 elements)");
-            }
-        }
-        check_kv_rows(k, v, 0, D);
         require_device(q, "q");
         require_device(k, "k");
         require_device(v, "v");
@@ -1499,12 +1522,24 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         const Options opt = normalize_options(has_scale, scale, causal_eff, window_left, window_right,
                                               softcap, D, max_seqlen_k);
         const DropoutArgs drop = parse_dropout(dropout, softcap, q);
+        // Packed copies of what the tile loads cannot use (host/layout.rs:46-125).
+        Staged sq_(q, s, true), sk_(k, s, true, 0, D), sv_(v, s, true, 0, D);
+        Staged so_(out, s, zero_tensors == 0, -1, 0, {q, k, v});
+        q = sq_.get();
+        k = sk_.get();
+        v = sv_.get();
+        out = so_.get();
         if (zero_tensors || max_seqlen_k == 0) {
             // varlen/mod.rs:418-443: cleared output, LSE -inf (+inf without keys).
-            zero_rows(out->data, Tq, H * D, out->strides[0], s);
+            for (int64_t hi = 0; hi < H; ++hi) {
+                zero_rows(static_cast<uint16_t*>(out->data) + hi * out->strides[1], Tq, D, out->strides[0], s);
+            }
             fill_f32(static_cast<float*>(lse->data), H * Tq, max_seqlen_k == 0 ? INFINITY : -INFINITY, s);
         }
-        if (Tq == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) return;
+        if (Tq == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) {
+            so_.copy_out();
+            return;
+        }
         FwdParams prm{};
         prm.q = q->data;
         prm.k = k->data;
@@ -1541,6 +1576,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         launch_fwd<true>(prm, q->dtype, bucket_for(D), general, s);
+        so_.copy_out();
     });
 }
 

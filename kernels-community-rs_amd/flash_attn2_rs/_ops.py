@@ -105,25 +105,17 @@ def _fwd_impl(args, lse_only):
     if q.ndim != 4:
         raise ValueError(f"q must have 4 dimensions [B, S, H, D], got shape {list(q.shape)}")
     b, sq, h, d = q.shape
-    qp, kp, vp = _packed(q), _packed(k), _packed(v)
-    copy_out = supplied is not None and (
-        supplied.stride(-1) != 1 or not _rows_aligned(supplied)
-        or any(supplied.data_ptr() == t.data_ptr() for t in (q, k, v))
-    )
-    out = supplied if supplied is not None and not copy_out else torch.empty(
-        q.shape, dtype=q.dtype, device=q.device)
-    if supplied is not None and (supplied.shape != q.shape or supplied.dtype != q.dtype):
-        raise ValueError("out must match q's shape, dtype and device")
+    # Misaligned or strided inputs and an output that the kernels cannot write
+    # in place are staged through packed copies inside the C ABI
+    # (host/layout.rs:46-125, host/forward/mod.rs:349-376).
+    out = supplied if supplied is not None else torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((b, h, sq), dtype=torch.float32, device=q.device)
     has_scale, sc = _scale_args(scale)
-    descs = [describe(t) for t in (qp, kp, vp, alibi)]
+    descs = [describe(t) for t in (q, k, v, alibi)]
     keep_alive, drop = dropout_arg(p, seed, offset, state)
     call("kcr_flash_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
          ctypes.c_int64(int(wl)), ctypes.c_int64(int(wr)), ctypes.c_double(float(softcap)), drop,
          ref(describe(out)), ref(describe(lse)), stream_of(q))
-    if copy_out:
-        supplied.copy_(out)
-        out = supplied
     return lse if lse_only else [out, lse]
 
 
@@ -161,11 +153,10 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
             and float(np.float32(p)) == 0.0 and int(left) < 0 and int(right) < 0):
         return _grouped_decode(q, k, v, cu_seqlens_k, seqused_k, leftpad_k, scale, softcap, max_k,
                                zero_tensors)
-    qp, kp, vp = _packed(q), _packed(k), _packed(v)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
     has_scale, sc = _scale_args(scale)
-    descs = [describe(t) for t in (qp, kp, vp, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi)]
+    descs = [describe(t) for t in (q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi)]
     keep_alive, drop = dropout_arg(p, 0, 0, state)
     call("kcr_flash_varlen_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
          ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)), drop,
@@ -189,7 +180,7 @@ def _grouped_decode(q, k, v, cu_seqlens_k, seqused_k, leftpad_k, scale, softcap,
     lse_g = torch.empty((hk, b * g), dtype=torch.float32, device=q.device)
     has_scale, sc = _scale_args(scale)
     call("kcr_flash_varlen_fwd", *(ref(describe(t)) for t in (
-             qg, _packed(k), _packed(v), cu_q, cu_seqlens_k, seqused_k, leftpad_k, None)),
+             qg, k, v, cu_q, cu_seqlens_k, seqused_k, leftpad_k, None)),
          has_scale, sc, 0, ctypes.c_int64(-1), ctypes.c_int64(-1), ctypes.c_double(float(softcap)), None,
          ctypes.c_int64(g), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)), ref(describe(out_g)),
          ref(describe(lse_g)), stream_of(q))
@@ -231,7 +222,7 @@ def bwd_preprocess(dout, out, p):
     b, s, h, d = out.shape
     rounded = (s + 127) // 128 * 128
     delta = torch.empty((b, h, rounded), dtype=torch.float32, device=out.device)
-    call("kcr_flash_bwd_preprocess", ref(describe(_packed(dout))), ref(describe(_packed(out))),
+    call("kcr_flash_bwd_preprocess", ref(describe(dout)), ref(describe(out)),
          ctypes.c_double(float(p)), ref(describe(delta)), stream_of(out))
     return delta
 
@@ -253,7 +244,7 @@ def _bwd(args, want_q, want_kv):
             raise ValueError("dropout backward requires saved RNG state")
         if not _rng_state_ok(rng, q):
             raise ValueError("RNG state must be contiguous CUDA int64 [2] on q's device")
-    qp, kp, vp, dp = _packed(q), _packed(k), _packed(v), _packed(dout)
+    qp, kp, vp, dp = q, k, v, dout
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device) if want_q else None
     dk = torch.empty(k.shape, dtype=k.dtype, device=k.device) if want_kv else None
     dv = torch.empty(v.shape, dtype=v.dtype, device=v.device) if want_kv else None
@@ -294,7 +285,7 @@ def varlen_bwd_explicit(q, k, v, dout, out, lse, cu_seqlens_q, cu_seqlens_k, ali
             raise ValueError("dropout backward requires saved RNG state")
         if not _rng_state_ok(state, q):
             raise ValueError("RNG state must be contiguous CUDA int64 [2] on q's device")
-    qp, kp, vp, dp, op = (_packed(t) for t in (q, k, v, dout, out))
+    qp, kp, vp, dp, op = q, k, v, dout, out
     batch = cu_seqlens_q.numel() - 1
     tq, h, d = q.shape
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
