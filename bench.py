@@ -18,6 +18,7 @@ Prints ONE JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -263,9 +264,8 @@ def wl_fa_kvcache_decode():
 
 
 def wl_hbm_copy():
-    """Plain device copy of the activation input size (939,524,096 B read and
-    written): the known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE
-    counters, and the practical HBM ceiling beside the 8 TB/s peak."""
+    """Plain device copy (torch `copy_`) of the activation input size
+    (939,524,096 B read and written), for comparison with the streaming probe."""
     g = _gen(2)
     x = torch.randn(16384, 28672, generator=g).bfloat16().cuda()
     y = torch.empty_like(x)
@@ -275,6 +275,80 @@ def wl_hbm_copy():
 
     return dict(run=run, work=2 * x.numel() * 2, bound="hbm", kernel="elementwise_kernel",
                 config={"x": list(x.shape), "dtype": "bf16"}, cpu=None)
+
+
+def _wl_hbm_stream(reads):
+    """The HBM ceiling the bandwidth-bound ops can reach: `kcr_hbm_stream_probe`,
+    the gated kernel's memory shape with no arithmetic. reads=1 copies the
+    RMSNorm-sized 134,217,728 B (1:1 read:write, like RMSNorm forward); reads=2
+    reads the gated input's 939,524,096 B and writes half of it (2:1, like
+    silu_and_mul)."""
+
+    def make():
+        import kcr_native
+
+        if reads == 1:
+            words = 16384 * 4096 * 2 // 16
+        else:
+            words = 16384 * 14336 * 2 // 16
+        src = torch.empty(reads * words * 16, dtype=torch.uint8, device="cuda").random_(0, 256)
+        dst = torch.empty(words * 16, dtype=torch.uint8, device="cuda")
+        fn = kcr_native.lib.kcr_hbm_stream_probe
+
+        def run():
+            stream = kcr_native.stream_of(dst)
+            kcr_native.check(fn(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                                ctypes.c_int64(words), ctypes.c_int32(reads), stream))
+
+        return dict(run=run, work=(reads + 1) * words * 16, bound="hbm", kernel="hbm_stream_kernel",
+                    config={"read_bytes": reads * words * 16, "write_bytes": words * 16,
+                            "read_write": f"{reads}:1"}, cpu=None)
+
+    return make
+
+
+def wl_fa_split():
+    """Short queries against long keys (an underfilled grid without key splits):
+    B=1, Hq=8, Hkv=2, Sq=128, Sk=32768, D=128, causal bf16. 8 query tiles alone
+    would occupy 8 of the 256 CUs."""
+    import flash_attn2_rs
+
+    b, hq, hkv, sq, sk, d = 1, 8, 2, 128, 32768, 128
+    g = _gen(8)
+    q = torch.randn(b, sq, hq, d, generator=g).bfloat16().cuda()
+    k = torch.randn(b, sk, hkv, d, generator=g).bfloat16().cuda()
+    v = torch.randn(b, sk, hkv, d, generator=g).bfloat16().cuda()
+    out = torch.empty_like(q)
+    ops = flash_attn2_rs.ops
+
+    def run():
+        ops.fwd_lse(q, k, v, None, None, True, -1, -1, 0.0, out)
+
+    # Causal with Sk > Sq: row i sees Sk - Sq + i + 1 keys.
+    pairs = sum(sk - sq + i + 1 for i in range(sq))
+    return dict(run=run, work=4.0 * b * hq * d * pairs, bound="mfma", kernel="flash_fwd_tiled",
+                config={"B": b, "Hq": hq, "Hkv": hkv, "Sq": sq, "Sk": sk, "D": d, "causal": True,
+                        "dtype": "bf16"}, cpu=None)
+
+
+def wl_fa_config1():
+    """BASELINE.json configs[0], the reference's CPU-runnable case: B=1,
+    Hq=Hkv=4, S=128, D=64, causal bf16. On the GPU it is launch-bound; the CPU
+    baseline times it in full."""
+    import flash_attn2_rs
+
+    b, h, s, d = 1, 4, 128, 64
+    q, k, v = _attn_inputs(0, b, h, h, s, d)
+    out = torch.empty_like(q)
+    ops = flash_attn2_rs.ops
+
+    def run():
+        ops.fwd_lse(q, k, v, None, None, True, -1, -1, 0.0, out)
+
+    flops = 4.0 * b * h * s * s * d * 0.5
+    return dict(run=run, work=flops, bound="mfma", kernel="flash_fwd",
+                config={"B": b, "Hq": h, "Hkv": h, "S": s, "D": d, "causal": True, "dtype": "bf16"},
+                cpu=lambda: cpu_attention(q, k, v, True, full=True))
 
 
 WORKLOADS = {
@@ -293,14 +367,30 @@ WORKLOADS = {
     "gelu_tanh_and_mul": _wl_gated("gelu_tanh_and_mul"),
     "silu": wl_silu,
     "fa_kvcache_decode": wl_fa_kvcache_decode,
+    "fa_fwd_split": wl_fa_split,
+    "fa_fwd_config1": wl_fa_config1,
+    "hbm_stream_1to1": _wl_hbm_stream(1),
+    "hbm_stream_2to1": _wl_hbm_stream(2),
     "hbm_copy": wl_hbm_copy,
 }
 DEFAULT_ORDER = [n for n in WORKLOADS if n != "hbm_copy"]
+# Ops whose CPU baseline is timed in every default run (bounded samples).
+CPU_OPS = ("fa_fwd_causal", "fa_fwd_config1", "rms_norm", "silu_and_mul")
 
 # --------------------------------------------------------------------------
 # CPU baselines: the oracle (the tests' formulas restated in numpy), timed on a
 # bounded sample on this host, scaled to the metric's unit.
 # --------------------------------------------------------------------------
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def _timed(fn, min_runs=3, budget_s=8.0):
@@ -315,6 +405,16 @@ def _timed(fn, min_runs=3, budget_s=8.0):
     return times[len(times) // 2]
 
 
+def _blas_threads():
+    """Threads numpy's BLAS uses (the attention oracle's matmuls run on them)."""
+    try:
+        from threadpoolctl import threadpool_info
+
+        return max([p["num_threads"] for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    except Exception:
+        return 1
+
+
 def cpu_gated(op, x):
     from oracle import activation as A
 
@@ -322,7 +422,8 @@ def cpu_gated(op, x):
     sample = x[:rows].float().cpu().numpy()
     t = _timed(lambda: A.gated(op, sample, "bf16"))
     bytes_ = rows * x.shape[1] * 2 * 1.5
-    return {"value": bytes_ / t / 1e9, "unit": "GB/s", "sample": f"oracle.activation.gated on {rows} of {x.shape[0]} rows"}
+    return {"value": bytes_ / t / 1e9, "unit": "GB/s", "cores": 1,
+            "sample": f"oracle.activation.gated on {rows} of {x.shape[0]} rows (numpy, element-wise)"}
 
 
 def cpu_rmsnorm(x, w):
@@ -333,21 +434,29 @@ def cpu_rmsnorm(x, w):
     wn = w.float().cpu().numpy()
     t = _timed(lambda: R.forward(sample, wn, 1e-6, 0.0, "llama", "bf16"))
     bytes_ = rows * x.shape[1] * 2 * 2
-    return {"value": bytes_ / t / 1e9, "unit": "GB/s", "sample": f"oracle.rmsnorm.forward on {rows} of {x.shape[0]} rows"}
+    return {"value": bytes_ / t / 1e9, "unit": "GB/s", "cores": 1,
+            "sample": f"oracle.rmsnorm.forward on {rows} of {x.shape[0]} rows (numpy, element-wise)"}
 
 
-def cpu_attention(q, k, v, causal):
+def cpu_attention(q, k, v, causal, full=False):
     from oracle import attention as OA
 
-    # One (batch, kv-group) slice: 4 query heads sharing one KV head, all 4096 rows.
-    qs = q[:1, :, :4].float().cpu().numpy()
-    ks = k[:1, :, :1].float().cpu().numpy()
-    vs = v[:1, :, :1].float().cpu().numpy()
+    if full:
+        qs, ks, vs = (t.float().cpu().numpy() for t in (q, k, v))
+        sample = f"oracle.attention.forward (numpy f32) on the whole call {list(q.shape)}"
+        heads = q.shape[0] * q.shape[2]
+    else:
+        # One (batch, kv-group) slice: 4 query heads sharing one KV head, all rows.
+        qs = q[:1, :, :4].float().cpu().numpy()
+        ks = k[:1, :, :1].float().cpu().numpy()
+        vs = v[:1, :, :1].float().cpu().numpy()
+        sample = (f"oracle.attention.forward (numpy f32) on batch 0, query heads 0-3 / KV head 0, "
+                  f"S={q.shape[1]}")
+        heads = 4
     t = _timed(lambda: OA.forward(qs, ks, vs, causal=causal), min_runs=2, budget_s=15.0)
     s, d = q.shape[1], q.shape[3]
-    flops = 4.0 * 4 * s * s * d * (0.5 if causal else 1.0)
-    return {"value": flops / t / 1e12, "unit": "TFLOP/s",
-            "sample": "oracle.attention.forward (numpy f32) on batch 0, query heads 0-3 / KV head 0, S=4096"}
+    flops = 4.0 * heads * s * s * d * (0.5 if causal else 1.0)
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "sample": sample}
 
 
 # --------------------------------------------------------------------------
@@ -418,21 +527,23 @@ def main():
         results[name] = {"value": round(achieved, 2), "unit": unit, "ms": round(ms, 4),
                          "frac_of_peak": round(achieved / peak, 4), "config": wl["config"]}
         log(f"[bench] {name}: {ms:.4f} ms, {achieved:.1f} {unit} ({achieved / peak:.1%} of peak)")
+        if not args.no_cpu and wl.get("cpu") is not None and (name in CPU_OPS or name == args.headline):
+            log(f"[bench] {name} cpu baseline ...")
+            cpu = wl["cpu"]()
+            cpu["kind"] = "port"
+            cpu["cpu"] = cpu_model()
+            cpu["value"] = round(cpu["value"], 4)
+            results[name]["cpu_baseline"] = cpu
+            log(f"[bench] {name} cpu: {cpu['value']} {cpu['unit']} on {cpu['cores']} thread(s)")
         if name == args.headline:
             headline = (wl, ms, achieved, peak, unit)
+        del wl
 
     if headline is None:
         print(json.dumps({"metric": METRIC, "value": None, "error": results.get(args.headline)}))
         sys.exit(1)
     wl, ms, achieved, peak, unit = headline
-    cpu = None
-    if not args.no_cpu and wl.get("cpu") is not None:
-        log("[bench] cpu baseline ...")
-        torch.set_num_threads(os.cpu_count() or 1)
-        cpu = wl["cpu"]()
-        cpu["cores"] = torch.get_num_threads()
-        cpu["kind"] = "port"
-        cpu["cpu"] = platform.processor() or platform.machine()
+    cpu = results[args.headline].get("cpu_baseline")
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():

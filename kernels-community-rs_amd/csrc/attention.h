@@ -469,6 +469,39 @@ struct TileLane {
     }
 };
 
+// The same reads with every per-lane part precomputed: one offset per K chunk
+// pair and per V^T column block (D / 16 + D / 16 registers), so a read costs one
+// add of the tile base, and the constant row offsets go into the instruction's
+// offset field. Used where the registers are free (the ping-pong forward); each
+// precomputed read saves the XOR and adds TileLane spends per read.
+template <int D>
+struct TileOffs {
+    static constexpr int KS = D / 16;
+    static constexpr int DB = D / 32;
+    int k[KS];     // row-major read of row l32, chunk 2 ks + hh
+    int vlo[DB];   // transposed read, rows 4 hh + li / 4, column block db
+    int vhi[DB];   // same, 8 rows further down
+
+    __device__ __forceinline__ TileOffs(int lane) {
+        const TileLane<D> tl(lane);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) k[ks] = tl.rm_base + 8 * ((2 * ks) ^ tl.rm_key);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            vlo[db] = tl.tr_base + 8 * ((4 * db) ^ tl.tr_key_lo);
+            vhi[db] = tl.tr_base + 8 * D + 8 * ((4 * db) ^ tl.tr_key_hi);
+        }
+    }
+    __device__ __forceinline__ u32x4 rm(const uint16_t* tile, int half, int ks) const {
+        return *reinterpret_cast<const u32x4*>(tile + k[ks] + 32 * half * D);
+    }
+    __device__ __forceinline__ u32x4 tr(const uint16_t* tile, int db, int tt) const {
+        const uint2 lo = ds_read_tr16(tile + vlo[db] + 16 * tt * D);
+        const uint2 hi = ds_read_tr16(tile + vhi[db] + 16 * tt * D);
+        return u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Dropout: FlashAttention-2's Philox4x32-7 stream (flash-attn2-rs/src/device/
 // dropout.rs:31-51). Element (query q, key k) of head bh = b * H + h is kept when

@@ -32,6 +32,7 @@
 
 #include "attention.h"
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -478,7 +479,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
     // query heads of one KV head share blockIdx % 8, i.e. one XCD and its L2.
     // Split-KV grids (packed sequences only): the splits of one query tile are
     // adjacent blocks.
-    const int nsplit = VARLEN && p.n_splits > 1 ? p.n_splits : 1;
+    const int nsplit = p.n_splits > 1 ? p.n_splits : 1;
     const int bid = static_cast<int>(blockIdx.x) / nsplit;
     const int split = static_cast<int>(blockIdx.x) - bid * nsplit;
     int b, head, qo;
@@ -545,6 +546,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         part_row0 = vs.qs;
         qb = (sq + BM - 1) / BM - 1 - qo;
         if (qb < 0) return;
+    } else {
+        part_row0 = b * sq;  // dense split partials: packed row b * Sq + row
     }
     const int row0 = qb * BM;
     if (row0 >= sq) return;
@@ -846,7 +849,7 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
     const int grp = (wave >> 2) ^ 1;
     const int l32 = lane & 31;
     const int hh = lane >> 5;
-    TileLane<D> tl(lane);
+    const TileOffs<D> to(lane);
 
     // Sequence-major order: the blocks of one (batch, KV head) run together and
     // share its K/V tiles in L2.
@@ -914,9 +917,9 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
         auto load = [&](auto ic) __attribute__((always_inline)) -> u32x4 {
             constexpr int i = decltype(ic)::value;
             if constexpr (i < NPV) {
-                return tl.tr(vl, i % DB, i / DB);
+                return to.tr(vl, i % DB, i / DB);
             } else {
-                return tl.rm(kl, (i - NPV) & 1, (i - NPV) >> 1);
+                return to.rm(kl, (i - NPV) & 1, (i - NPV) >> 1);
             }
         };
         // The MFMA-phase wave takes issue priority over the softmax-phase wave
@@ -924,7 +927,6 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
         // whichever phase it is in).
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        tl.refresh();
         if constexpr (QK) {
             sc[0] = f32x16{};
             sc[1] = f32x16{};
@@ -1097,6 +1099,8 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
 // per (head, packed row); lane l < D / 2 owns columns 2l and 2l + 1. Packed row
 // t is row t % rows_per_seq of sequence t / rows_per_seq in out / lse
 // (rows_per_seq = total_q with zero batch strides for packed outputs).
+constexpr uint32_t kUnseenLse = 0x7FC0DEADu;  // a quiet-NaN payload no kernel computes
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restrict__ o_part,
                                                            const float* __restrict__ lse_part, int n_splits,
@@ -1112,6 +1116,10 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restri
     const int head = static_cast<int>(item / total_q);
     const int row = static_cast<int>(item - static_cast<int64_t>(head) * total_q);
     const int64_t stride = static_cast<int64_t>(heads) * total_q;  // between splits
+    // Rows of no valid sequence keep the caller's output (plain varlen calls
+    // pre-fill the partial LSE with this payload; every block of a valid
+    // sequence overwrites it).
+    if (__float_as_uint(lse_part[item]) == kUnseenLse) return;
     float mx = -INFINITY;
     for (int i = 0; i < n_splits; ++i) mx = fmaxf(mx, lse_part[i * stride + item]);
     float acc[PER] = {};
@@ -1212,7 +1220,7 @@ void launch_tiled(FwdParams& prm, hipStream_t s) {
     constexpr int BM = 128;
     prm.q_blocks = (prm.seqlen_q + BM - 1) / BM;
     const int64_t blocks = static_cast<int64_t>(prm.q_blocks) * prm.batch * prm.heads *
-                           (VARLEN && prm.n_splits > 1 ? prm.n_splits : 1);
+                           (prm.n_splits > 1 ? prm.n_splits : 1);
     if (blocks == 0) return;
     if (blocks > INT32_MAX) throw value_error("attention grid exceeds the launch limit");
     prm.xcd_groups = ((static_cast<int64_t>(prm.batch) * prm.kv_heads) % 8 == 0) ? 1 : 0;
@@ -1256,7 +1264,8 @@ void launch_d(FwdParams& prm, bool general, hipStream_t s) {
             // (measured faster there; the 128-row tiled kernel wins on causal,
             // windowed, dropout, packed and D = 64 grids).
             if constexpr (D == 128 && !VARLEN) {
-                if (prm.window_left < 0 && prm.window_right < 0 && prm.drop_threshold == 255) {
+                if (prm.window_left < 0 && prm.window_right < 0 && prm.drop_threshold == 255 &&
+                    prm.n_splits <= 1) {
                     return launch_pp<T, D, VARLEN>(prm, s);
                 }
             }
@@ -1410,6 +1419,41 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
 
 namespace {
 
+// Merges the split partials of `prm` into its output and LSE; `rows` is the
+// packed-row count per batch entry (Sq for dense calls, Tq for packed ones).
+void launch_merge(const FwdParams& prm, int dtype, int bucket, int rows, hipStream_t s) {
+    const unsigned grid = static_cast<unsigned>((static_cast<int64_t>(prm.heads) * prm.total_q + 3) / 4);
+    auto merge = [&](auto tag) {
+        using T = decltype(tag);
+        if (bucket == 64) {
+            merge_splits_kernel<T, 64><<<grid, 256, 0, s>>>(
+                prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
+                static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
+        } else {
+            merge_splits_kernel<T, 128><<<grid, 256, 0, s>>>(
+                prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
+                static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
+        }
+    };
+    if (dtype == KCR_BFLOAT16) {
+        merge(bf16_t{});
+    } else {
+        merge(f16_t{});
+    }
+    check_launch("launch merge_splits");
+}
+
+// Key splits for a dense call whose query tiles cannot fill the chip: enough
+// splits for about two blocks per CU (the tiled kernel runs two per CU), each
+// split at least 256 keys, at most 32 (the reference's bounds,
+// host/forward/dispatch.rs:166-181). 1 means no split.
+int64_t dense_splits(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int cus) {
+    const int64_t blocks = (Sq + 127) / 128 * B * H;
+    if (Sk < 1024 || blocks >= cus || Sq * B * H > (int64_t{1} << 24)) return 1;
+    const int64_t want = (2 * cus + blocks - 1) / blocks;
+    return std::max<int64_t>(1, std::min<int64_t>({want, Sk / 256, 32}));
+}
+
 void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* alibi,
                    int32_t alibi_b, const Options& opt, const DropoutArgs& drop, int64_t B, int64_t Sq,
                    int64_t H, int64_t D, int64_t Sk, int64_t Hk, const kcr_tensor* out,
@@ -1455,7 +1499,28 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
         set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
-        launch_fwd<false>(prm, q->dtype, bucket_for(D), general, s);
+        const int bucket = bucket_for(D);
+        const int64_t splits = (general || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
+                                   ? 1
+                                   : dense_splits(B, H, Sq, Sk, compute_units());
+        if (splits <= 1) {
+            launch_fwd<false>(prm, q->dtype, bucket, general, s);
+            return;
+        }
+        // Key splits for an underfilled grid (host/forward/dispatch.rs:127-238
+        // plans the same trade): fp32 partials [splits, H, B * Sq, D] and
+        // [splits, H, B * Sq] from the stream-ordered allocator, then the merge.
+        const int64_t rows = B * Sq;
+        const int64_t bytes = splits * H * rows * (bucket + 1) * static_cast<int64_t>(sizeof(float));
+        void* ws = nullptr;
+        check_hip(hipMallocAsync(&ws, static_cast<size_t>(bytes), s), "hipMallocAsync (split partials)");
+        prm.n_splits = static_cast<int32_t>(splits);
+        prm.total_q = static_cast<int32_t>(rows);
+        prm.o_part = static_cast<float*>(ws);
+        prm.lse_part = prm.o_part + splits * H * rows * bucket;
+        launch_fwd<false>(prm, q->dtype, bucket, false, s);
+        launch_merge(prm, q->dtype, bucket, static_cast<int>(Sq), s);
+        check_hip(hipFreeAsync(ws, s), "hipFreeAsync (split partials)");
     }
 }
 
@@ -1575,7 +1640,26 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
         set_dropout(prm, drop);
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
-        launch_fwd<true>(prm, q->dtype, bucket_for(D), general, s);
+        const int bucket = bucket_for(D);
+        const int64_t splits = (general || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
+                                   ? 1
+                                   : dense_splits(batch, H, max_seqlen_q, max_seqlen_k, compute_units());
+        if (splits <= 1) {
+            launch_fwd<true>(prm, q->dtype, bucket, general, s);
+        } else {
+            // Key splits for an underfilled packed grid, as for dense calls; rows
+            // of no valid sequence are left as they are (see merge_splits_kernel).
+            const int64_t bytes = splits * H * Tq * (bucket + 1) * static_cast<int64_t>(sizeof(float));
+            void* ws = nullptr;
+            check_hip(hipMallocAsync(&ws, static_cast<size_t>(bytes), s), "hipMallocAsync (split partials)");
+            prm.n_splits = static_cast<int32_t>(splits);
+            prm.o_part = static_cast<float*>(ws);
+            prm.lse_part = prm.o_part + splits * H * Tq * bucket;
+            fill_f32(prm.lse_part, H * Tq, __builtin_bit_cast(float, kUnseenLse), s);
+            launch_fwd<true>(prm, q->dtype, bucket, false, s);
+            launch_merge(prm, q->dtype, bucket, static_cast<int>(Tq), s);
+            check_hip(hipFreeAsync(ws, s), "hipFreeAsync (split partials)");
+        }
         so_.copy_out();
     });
 }

@@ -549,9 +549,10 @@ __global__ void __launch_bounds__(64 * kReduceWaves) reduce_weight_grad(W* __res
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const uint32_t c = blockIdx.x * 64 + lane;
-    const uint32_t per = (blocks + kReduceWaves - 1) / kReduceWaves;
-    const uint32_t b0 = min(static_cast<uint32_t>(wave) * per, blocks);
-    const uint32_t b1 = min(b0 + per, blocks);
+    // 64-bit so that blocks near 2^32 cannot wrap the run length to zero.
+    const uint64_t per = (static_cast<uint64_t>(blocks) + kReduceWaves - 1) / kReduceWaves;
+    const uint32_t b0 = static_cast<uint32_t>(min(static_cast<uint64_t>(wave) * per, static_cast<uint64_t>(blocks)));
+    const uint32_t b1 = static_cast<uint32_t>(min(static_cast<uint64_t>(b0) + per, static_cast<uint64_t>(blocks)));
     float sum = 0.0f;
     if (c < n) {
         uint32_t b = b0;

@@ -1,4 +1,4 @@
-"""The C ABI: libkcr_hip.so loads, exports every symbol include/kcr_hip.h
+"""The C ABI: libkcr_hip.so loads, exports every symbol include/*.h
 declares, and validates arguments (with the reference's error texts) before
 touching any device memory -- so these run on the CPU."""
 
@@ -12,7 +12,7 @@ ROOT = Path(__file__).resolve().parent.parent
 
 
 def declared_symbols():
-    text = (ROOT / "include" / "kcr_hip.h").read_text()
+    text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(kcr_[a-z0-9_]+)\s*\(", text)))
 
