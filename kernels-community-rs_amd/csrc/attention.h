@@ -502,6 +502,26 @@ struct TileOffs {
     }
 };
 
+constexpr int kBN = 64;               // keys per K/V tile of the forward kernels
+constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag behind
+
+// Slot boundary: this wave's LDS reads are complete, then the block barrier.
+// The asm memory clobber keeps memory operations on their side; the scheduling
+// barriers keep every other instruction on its side too.
+__device__ __forceinline__ void slot_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt at their maximum (gfx9 encoding:
+// vmcnt bits 3:0 in bits 3:0, bits 5:4 in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // ---------------------------------------------------------------------------
 // Dropout: FlashAttention-2's Philox4x32-7 stream (flash-attn2-rs/src/device/
 // dropout.rs:31-51). Element (query q, key k) of head bh = b * H + h is kept when

@@ -39,7 +39,6 @@
 namespace kcr {
 namespace attn {
 
-constexpr int kBN = 64;  // keys per tile
 
 // V^T tile rows hold 16 chunks of 4 keys (8 bytes). The loading threads write
 // one chunk to each of 16 rows that are 8 apart; XOR-ing the chunk index with
@@ -50,7 +49,6 @@ __device__ __forceinline__ int vt_swizzle(int row) {
     const int x = (row >> 4) & 7;
     return (x & 1) | ((x & 6) << 1);
 }
-constexpr float kRescaleSlack = 8.0f;  // log2 units the running max may lag behind
 constexpr int kLookTiled = 3;          // operand reads in flight ahead of their MFMA (tiled kernel)
 
 // GENERAL covers softcap, ALiBi and head sizes below the compiled bucket (zeroed
@@ -810,22 +808,6 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
 // ---------------------------------------------------------------------------
 constexpr int kPPStages = 4;
 
-
-// Slot boundary: this wave's LDS reads are complete, then the block barrier.
-// The asm memory clobber keeps memory operations on their side; the scheduling
-// barriers keep every other instruction on its side too.
-__device__ __forceinline__ void slot_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// s_waitcnt vmcnt(N) with expcnt / lgkmcnt at their maximum (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmem_le() {
-    static_assert(N >= 0 && N < 16, "vmcnt immediate");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
-}
 
 template <typename T, int D>
 __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p) {
