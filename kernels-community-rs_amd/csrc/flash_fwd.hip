@@ -1102,21 +1102,42 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restri
     // pre-fill the partial LSE with this payload; every block of a valid
     // sequence overwrites it).
     if (__float_as_uint(lse_part[item]) == kUnseenLse) return;
-    float mx = -INFINITY;
-    for (int i = 0; i < n_splits; ++i) mx = fmaxf(mx, lse_part[i * stride + item]);
+    // Lane i holds the LSE of splits i and i + 64 (n_splits <= 128): one load
+    // each, wave reductions for the max and the sum, then the O rows of the
+    // splits eight at a time with their loads issued together.
+    const float l0 = lane < n_splits ? lse_part[lane * stride + item] : -INFINITY;
+    const float l1 = lane + 64 < n_splits ? lse_part[(lane + 64) * stride + item] : -INFINITY;
+    float mx = fmaxf(l0, l1);
+#pragma unroll
+    for (int sh = 32; sh > 0; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 64));
     float acc[PER] = {};
     float out_lse = INFINITY;
     if (mx > -INFINITY) {
-        float sum = 0.0f;
-        for (int i = 0; i < n_splits; ++i) sum += expf(lse_part[i * stride + item] - mx);
+        float sum = expf(l0 - mx) + expf(l1 - mx);
+#pragma unroll
+        for (int sh = 32; sh > 0; sh >>= 1) sum += __shfl_xor(sum, sh, 64);
         out_lse = mx + logf(sum);
-        for (int i = 0; i < n_splits; ++i) {
-            const float w = expf(lse_part[i * stride + item] - out_lse);
-            if (w == 0.0f) continue;
-            if (lane < D / 2) {
-                const float* src = o_part + (i * stride + item) * D + PER * lane;
-                acc[0] += w * src[0];
-                acc[1] += w * src[1];
+        const float w0 = expf(l0 - out_lse), w1 = expf(l1 - out_lse);
+        const int col = PER * (lane < D / 2 ? lane : 0);
+        for (int i0 = 0; i0 < n_splits; i0 += 8) {
+            float w[8];
+            float2 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u;
+                w[u] = i < 64 ? __shfl(w0, i & 63, 64) : __shfl(w1, i & 63, 64);
+                // A split that saw no key of the row has weight 0 and may hold
+                // no partial row at all: its values are never used.
+                v[u] = (i < n_splits && w[u] != 0.0f)
+                           ? *reinterpret_cast<const float2*>(o_part + (i * stride + item) * D + col)
+                           : float2{0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (i0 + u < n_splits && w[u] != 0.0f) {
+                    acc[0] += w[u] * v[u].x;
+                    acc[1] += w[u] * v[u].y;
+                }
             }
         }
     }
