@@ -14,7 +14,10 @@ ROOT = Path(__file__).resolve().parent.parent
 def declared_symbols():
     text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(kcr_[a-z0-9_]+)\s*\(", text)))
+    names = set(re.findall(r"\b(kcr_[a-z0-9_]+)\s*\(", text))
+    # KCR_TVM_FFI_EXPORT(name) declares __tvm_ffi_<name>.
+    names |= {"__tvm_ffi_" + n for n in re.findall(r"^KCR_TVM_FFI_EXPORT\((\w+)\)", text, flags=re.M)}
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
@@ -22,6 +25,7 @@ def test_library_exports_every_declared_symbol():
 
     names = declared_symbols()
     assert "kcr_silu_and_mul" in names and "kcr_rms_norm_forward" in names
+    assert "__tvm_ffi_fwd_lse" in names and "kcr_hbm_stream_probe" in names
     missing = [n for n in names if not hasattr(kcr_native.lib, n)]
     assert not missing, missing
     assert "gfx950" in kcr_native.version()
