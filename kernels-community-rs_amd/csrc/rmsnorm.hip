@@ -205,7 +205,7 @@ constexpr int kWaves = 4;  // waves per block of the wave-per-row kernel
 // (l >= 32): the lane keeps one partial per slot and the 32-lane butterflies
 // give the warp sums. Requires n % 8 == 0, 16-byte aligned tensors and (with
 // AFFINE) a weight of X's type or f32.
-template <typename X, typename W, int M, bool AFFINE, int CHUNKS, int SLOTS>
+template <typename X, typename W, int M, bool AFFINE, int CHUNKS, int SLOTS, bool WLDS>
 __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
     X* __restrict__ y, float* __restrict__ rstd_out, const X* __restrict__ x,
     const W* __restrict__ weight, uint32_t rows, uint32_t groups, float inv_n, float eps,
@@ -218,18 +218,37 @@ __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
     const uint32_t waves = gridDim.x * kWaves;
     const uint32_t n = groups * 8;
 
-    u32x4 wv[AFFINE ? CHUNKS * WV : 1];
+    u32x4 wv[AFFINE && !WLDS ? CHUNKS * WV : 1];
+    __shared__ u32x4 w_lds[AFFINE && WLDS ? CHUNKS * WV * 64 : 1];
     if constexpr (AFFINE) {
         const u32x4* wp = reinterpret_cast<const u32x4*>(weight);
+        if constexpr (WLDS) {
+            // The weight staged once per block, lane-contiguous per chunk.
+            for (uint32_t i = threadIdx.x; i < CHUNKS * WV * 64u; i += 64u * kWaves) {
+                const uint32_t c = i / (64u * WV), rest = i - c * 64u * WV;
+                const uint32_t h = rest / 64u, l = rest - h * 64u;
+                const uint32_t g = l + 64u * c;
+                if (g < groups) w_lds[i] = wp[g * WV + h];
+            }
+            __syncthreads();
+        } else {
 #pragma unroll
-        for (int c = 0; c < CHUNKS; ++c) {
-            const uint32_t g = lane + 64u * c;
+            for (int c = 0; c < CHUNKS; ++c) {
+                const uint32_t g = lane + 64u * c;
 #pragma unroll
-            for (int h = 0; h < WV; ++h) {
-                if (g < groups) wv[c * WV + h] = wp[g * WV + h];
+                for (int h = 0; h < WV; ++h) {
+                    if (g < groups) wv[c * WV + h] = wp[g * WV + h];
+                }
             }
         }
     }
+    auto weight_vec = [&](int c, int h) -> u32x4 {
+        if constexpr (WLDS) {
+            return w_lds[(c * WV + h) * 64 + lane];
+        } else {
+            return wv[c * WV + h];
+        }
+    };
 
     // Rows are dealt to waves round-robin; the next row's loads are issued
     // before the current row is reduced and written, so every wave keeps a
@@ -290,10 +309,10 @@ __global__ void __launch_bounds__(64 * kWaves) rms_fwd_wave(
                 widen_x(xv, c, f);
                 if constexpr (AFFINE) {
                     if constexpr (WV == 2) {
-                        widen16<float>(wv[2 * c], w);
-                        widen16<float>(wv[2 * c + 1], w + 4);
+                        widen16<float>(weight_vec(c, 0), w);
+                        widen16<float>(weight_vec(c, 1), w + 4);
                     } else {
-                        widen16<W>(wv[c], w);
+                        widen16<W>(weight_vec(c, 0), w);
                     }
                 }
 #pragma unroll
@@ -663,12 +682,18 @@ template <typename X, typename W, int M, bool AFFINE, int CHUNKS, int SLOTS>
 void launch_wave(const Fwd& f, uint32_t groups) {
     const uint64_t waves_needed = static_cast<uint64_t>(f.rows);
     uint64_t blocks = (waves_needed + kWaves - 1) / kWaves;
-    // Six blocks (24 waves) per CU, each wave looping over rows with one row
-    // prefetched: measured on MI355X at 16384 x 4096 bf16, 50 us for one
-    // wave per row vs 45.5 us for this shape.
-    const uint64_t cap = 6ull * compute_units();
+    // Each wave loops over rows with the next row prefetched; shorter rows run
+    // six blocks (24 waves) per CU (one wave per row measured 50 us against
+    // 45.5 us for this at 16384 x 4096 bf16 with the weight in registers).
+    // Rows of 8 or more chunks (n >= 4096 at 16 bits) stage the weight in LDS
+    // instead of registers (184 -> 122 VGPRs at n = 4096 bf16, 2 -> 4 waves per
+    // SIMD) and run up to 16 blocks per CU: 44.0 us against 44.9 us for the
+    // register weight at 6 blocks per CU (16384 x 4096 bf16; 12 / 24 / one-shot
+    // grids 44.6 / 44.1 / 44.1 us).
+    constexpr bool WLDS = CHUNKS >= 8;
+    const uint64_t cap = (WLDS ? 16ull : 6ull) * compute_units();
     if (blocks > cap) blocks = cap;
-    rms_fwd_wave<X, W, M, AFFINE, CHUNKS, SLOTS><<<static_cast<unsigned>(blocks), 64 * kWaves, 0, f.stream>>>(
+    rms_fwd_wave<X, W, M, AFFINE, CHUNKS, SLOTS, WLDS><<<static_cast<unsigned>(blocks), 64 * kWaves, 0, f.stream>>>(
         static_cast<X*>(f.y->data), static_cast<float*>(f.rstd->data),
         static_cast<const X*>(f.x->data),
         static_cast<const W*>(AFFINE ? f.w->data : f.x->data), static_cast<uint32_t>(f.rows),
