@@ -735,30 +735,46 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
         const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
                                (wl >= 0 && kb < last_row + off - wl);
         u32x4 pk[4];
+        // The mask test is hoisted out of the element loop: one branch per
+        // tile instead of a scalar branch per element.
+        // MASK: 0 none, 1 masked, 2 tested per element (the dropout kernels,
+        // where two copies of the loop would spill).
+        auto ds_tile = [&](auto mask_tag) __attribute__((always_inline)) {
+            constexpr int MASK = decltype(mask_tag)::value;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            float dsv[16];
-            uint32_t keep_bits = 0xFFFFu;
-            if constexpr (DROPOUT) {
-                keep_bits = keep_bits_query_lane_shared(drop, bh, static_cast<uint32_t>(my_row),
-                                                 static_cast<uint32_t>(kb / 32 + sub), hh);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float pr = fast_exp2(__builtin_fmaf(s[sub][r], c, -lse2));
-                if (need_mask) {
-                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    const bool masked = (col >= sk) | (wr >= 0 & col > my_row + off + wr) |
-                                        (wl >= 0 & col < my_row + off - wl);
-                    pr = masked ? 0.0f : pr;
+            for (int sub = 0; sub < 2; ++sub) {
+                float dsv[16];
+                uint32_t keep_bits = 0xFFFFu;
+                if constexpr (DROPOUT) {
+                    keep_bits = keep_bits_query_lane_shared(drop, bh, static_cast<uint32_t>(my_row),
+                                                     static_cast<uint32_t>(kb / 32 + sub), hh);
                 }
-                dsv[r] = pr * ((((keep_bits >> r) & 1u) ? dp[sub][r] : 0.0f) - dlt);
-            }
 #pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2) {
+                for (int r = 0; r < 16; ++r) {
+                    float pr = fast_exp2(__builtin_fmaf(s[sub][r], c, -lse2));
+                    if (MASK == 1 || (MASK == 2 && need_mask)) {
+                        const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        const bool masked = (col >= sk) | (wr >= 0 & col > my_row + off + wr) |
+                                            (wl >= 0 & col < my_row + off - wl);
+                        pr = masked ? 0.0f : pr;
+                    }
+                    dsv[r] = pr * ((((keep_bits >> r) & 1u) ? dp[sub][r] : 0.0f) - dlt);
+                }
 #pragma unroll
-                for (int w = 0; w < 4; ++w) pk[2 * sub + t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
+                for (int t2 = 0; t2 < 2; ++t2) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        pk[2 * sub + t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
+                    }
+                }
             }
+        };
+        if constexpr (DROPOUT) {
+            ds_tile(std::integral_constant<int, 2>{});
+        } else if (need_mask) {
+            ds_tile(std::integral_constant<int, 1>{});
+        } else {
+            ds_tile(std::integral_constant<int, 0>{});
         }
         // dQ^T += K^T dS^T (K^T read transposed from the key tile); step i:
         // db = i % DB, tt = i / DB, reads ahead as above.
@@ -972,27 +988,62 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                 keep_bits = keep_bits_key_lane_shared(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + (t % gqa)),
                                                static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh);
             }
+            // The mask test is hoisted out of the element loop: one branch per
+            // tile instead of a scalar branch per element.
+            auto p_ds = [&](auto mask_tag) __attribute__((always_inline)) {
+                constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int qloc = 32 * qc + 8 * g + 4 * hh;
-                const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
-                const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
-                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+                for (int g = 0; g < 4; ++g) {
+                    const int qloc = 32 * qc + 8 * g + 4 * hh;
+                    const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
+                    const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * g + e;
-                    float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
-                    if (need_mask) {
-                        const int row = qb + qloc + e;
-                        const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
-                                            (wl >= 0 & my_key < row + off - wl);
-                        pr = masked ? 0.0f : pr;
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * g + e;
+                        float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                        if constexpr (MASK) {
+                            const int row = qb + qloc + e;
+                            const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
+                                                (wl >= 0 & my_key < row + off - wl);
+                            pr = masked ? 0.0f : pr;
+                        }
+                        const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                        pv[r] = kept ? pr : 0.0f;
+                        dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
                     }
-                    const bool kept = ((keep_bits >> r) & 1u) != 0u;
-                    pv[r] = kept ? pr : 0.0f;
-                    dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
                 }
+            };
+            if constexpr (DROPOUT) {
+                // The dropout kernel keeps the per-element test inline: through
+                // the lambda it spills.
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int qloc = 32 * qc + 8 * g + 4 * hh;
+                    const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
+                    const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * g + e;
+                        float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                        if (need_mask) {
+                            const int row = qb + qloc + e;
+                            const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
+                                                (wl >= 0 & my_key < row + off - wl);
+                            pr = masked ? 0.0f : pr;
+                        }
+                        const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                        pv[r] = kept ? pr : 0.0f;
+                        dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
+                    }
+                }
+            } else if (need_mask) {
+                p_ds(std::true_type{});
+            } else {
+                p_ds(std::false_type{});
             }
 #pragma unroll
             for (int t2 = 0; t2 < 2; ++t2) {
