@@ -913,39 +913,78 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
     const int ntiles = nqb * gqa;
     const float c = p.scale_log2;
 
-    auto tile_row0 = [&](int t) { return q_begin + (nqb - 1 - t / gqa) * BQ; };
-    auto copy_tile = [&](int t, int stage) {
-        const int j = t % gqa;
-        const int qb = tile_row0(t);
-        const int head = kvh * p.gqa + j;
-        const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head * p.q_h;
-        const uint16_t* dobase = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) + head * p.do_h;
-        copy_rows_dma<D, NW, BQ>(qbase + static_cast<int64_t>(qb) * p.q_s, p.q_s, sq - qb, q_lds + stage * TILE, wave, lane);
-        copy_rows_dma<D, NW, BQ>(dobase + static_cast<int64_t>(qb) * p.do_s, p.do_s, sq - qb, do_lds + stage * TILE, wave, lane);
-        // Rows past the sequence read LSE 0 and delta 0; their Q and dO rows are
-        // zero, so they add nothing to dK and dV.
-        const uint32_t rows = static_cast<uint32_t>(max(0, min(sq - qb, BQ)));
-        if (wave == 0) {
-            const float* lse_row = p.lse + (VARLEN ? 0 : b * p.lse_b) + head * p.lse_h + sb.lse_row0 + qb;
-            dma_lds4(rsrc_words(lse_row, rows * 4u), lds_addr(lse_lds + stage * 64), lane * 4u);
-        } else if (wave == 1) {
-            const float* dl_row = p.delta + (VARLEN ? 0 : b * p.delta_b) + head * p.delta_h + sb.delta_row0 + qb;
-            dma_lds4(rsrc_words(dl_row, rows * 4u), lds_addr(dl_lds + stage * 64), lane * 4u);
+    // Tile t is query tile nqb - 1 - t / gqa (counted from q_begin) of query
+    // head kvh * gqa + t % gqa. The copies walk that order with a cursor of row
+    // pointers stepped per tile (no division or 64-bit multiply per tile).
+    struct Cursor {
+        int j, qb;  // head within the group, first query row of the tile
+        const uint16_t* q;
+        const uint16_t* dout;
+        const float* lse;
+        const float* delta;
+    };
+    const int qb_last = q_begin + (nqb - 1) * BQ;
+    Cursor cur;
+    {
+        const int head0 = kvh * gqa;
+        cur.j = 0;
+        cur.qb = qb_last;
+        cur.q = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head0 * p.q_h +
+                static_cast<int64_t>(qb_last) * p.q_s;
+        cur.dout = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) +
+                   head0 * p.do_h + static_cast<int64_t>(qb_last) * p.do_s;
+        cur.lse = p.lse + (VARLEN ? 0 : b * p.lse_b) + head0 * p.lse_h + sb.lse_row0 + qb_last;
+        cur.delta = p.delta + (VARLEN ? 0 : b * p.delta_b) + head0 * p.delta_h + sb.delta_row0 + qb_last;
+    }
+    // Steps when the head index wraps: back to the group's first head, one
+    // query tile down.
+    const int64_t q_wrap = -static_cast<int64_t>(gqa) * p.q_h - static_cast<int64_t>(BQ) * p.q_s;
+    const int64_t do_wrap = -static_cast<int64_t>(gqa) * p.do_h - static_cast<int64_t>(BQ) * p.do_s;
+    const int64_t lse_wrap = -static_cast<int64_t>(gqa) * p.lse_h - BQ;
+    const int64_t delta_wrap = -static_cast<int64_t>(gqa) * p.delta_h - BQ;
+    auto advance = [&](Cursor& c) {
+        ++c.j;
+        c.q += p.q_h;
+        c.dout += p.do_h;
+        c.lse += p.lse_h;
+        c.delta += p.delta_h;
+        if (c.j == gqa) {
+            c.j = 0;
+            c.qb -= BQ;
+            c.q += q_wrap;
+            c.dout += do_wrap;
+            c.lse += lse_wrap;
+            c.delta += delta_wrap;
         }
     };
-    if (ntiles > 0) copy_tile(0, 0);
+    auto copy_tile = [&](const Cursor& c, int stage) {
+        copy_rows_dma<D, NW, BQ>(c.q, p.q_s, sq - c.qb, q_lds + stage * TILE, wave, lane);
+        copy_rows_dma<D, NW, BQ>(c.dout, p.do_s, sq - c.qb, do_lds + stage * TILE, wave, lane);
+        // Rows past the sequence read LSE 0 and delta 0; their Q and dO rows are
+        // zero, so they add nothing to dK and dV.
+        const uint32_t rows = static_cast<uint32_t>(max(0, min(sq - c.qb, BQ)));
+        if (wave == 0) {
+            dma_lds4(rsrc_words(c.lse, rows * 4u), lds_addr(lse_lds + stage * 64), lane * 4u);
+        } else if (wave == 1) {
+            dma_lds4(rsrc_words(c.delta, rows * 4u), lds_addr(dl_lds + stage * 64), lane * 4u);
+        }
+    };
+    if (ntiles > 0) copy_tile(cur, 0);
     wait_vmem();
     __syncthreads();
+    int tj = 0, qb = qb_last;  // the computed tile's head index and first row
 
     for (int t = 0; t < ntiles; ++t) {
         tl.refresh();
         const int stage = t & 1;
-        const int qb = tile_row0(t);
         const uint16_t* ql = q_lds + stage * TILE;
         const uint16_t* dl = do_lds + stage * TILE;
         const float* lsl = lse_lds + stage * 64;
         const float* dll = dl_lds + stage * 64;
-        if (t + 1 < ntiles) copy_tile(t + 1, stage ^ 1);
+        if (t + 1 < ntiles) {
+            advance(cur);
+            copy_tile(cur, stage ^ 1);
+        }
 
         const bool need_mask = (key0 + BK > sk) || (wr >= 0 && key0 + BK - 1 > qb + off + wr) ||
                                (wl >= 0 && key0 < qb + BQ - 1 + off - wl);
@@ -985,7 +1024,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
             float pv[16], dsv[16];
             uint32_t keep_bits = 0xFFFFu;
             if constexpr (DROPOUT) {
-                keep_bits = keep_bits_key_lane_shared(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + (t % gqa)),
+                keep_bits = keep_bits_key_lane_shared(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + tj),
                                                static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh);
             }
             // The mask test is hoisted out of the element loop: one branch per
@@ -1077,6 +1116,10 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                 });
             }
+        }
+        if (++tj == gqa) {
+            tj = 0;
+            qb -= BQ;
         }
         wait_vmem();
         __syncthreads();
