@@ -611,7 +611,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2 * TILE];
     __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2 * TILE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar copy addresses
     const int l32 = lane & 31, hh = lane >> 5;
     TileLane<D> tl(lane);
 
@@ -840,7 +840,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
     __shared__ __attribute__((aligned(16))) float lse_lds[2 * 64];
     __shared__ __attribute__((aligned(16))) float dl_lds[2 * 64];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar copy addresses
     const int l32 = lane & 31, hh = lane >> 5;
     TileLane<D> tl(lane);
 

@@ -468,7 +468,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar copy addresses
     const int l32 = lane & 31;
     const int hh = lane >> 5;
     TileLane<D> tl(lane);
@@ -826,7 +826,7 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar copy addresses
     // Waves 4-7 lead (measured slightly faster than waves 0-3 leading).
     const int grp = (wave >> 2) ^ 1;
     const int l32 = lane & 31;
