@@ -684,41 +684,47 @@ __global__ void __launch_bounds__(128) rms_bwd_split(u32x4* dx, float* __restric
 }
 
 // dw[c] = sum_b dw_partial[b, c] in a fixed order, rounded to W (device.rs:339-358).
-// One block per 64 columns (a lane per column). Each of the 16 waves sums a
-// contiguous run of partial rows in order, with 8 loads in flight; wave 0 then
-// adds the 16 run sums in order. The order is fixed, so results repeat bit for
-// bit (it differs from one sequential chain only by fp32 rounding).
+// One block per 32 columns: each half-wave covers the 32 columns (128-byte
+// rows), the two halves taking alternate partial rows. Each of the 16 waves
+// sums a contiguous run of partial rows (8 loads in flight per lane), the
+// halves' sums are added, and wave 0 adds the 16 run sums in order. The order
+// is fixed, so results repeat bit for bit (it differs from one sequential
+// chain only by fp32 rounding).
 constexpr int kReduceWaves = 16;
+constexpr int kReduceCols = 32;  // columns per block: a half-wave each, 128-byte rows
 template <typename W>
 __global__ void __launch_bounds__(64 * kReduceWaves) reduce_weight_grad(W* __restrict__ dw,
                                                                         const float* __restrict__ dw_partial,
                                                                         uint32_t blocks, uint32_t n) {
-    __shared__ float run_sum[kReduceWaves][64];
+    __shared__ float run_sum[kReduceWaves][kReduceCols];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const uint32_t c = blockIdx.x * 64 + lane;
+    const int col = lane & (kReduceCols - 1);
+    const int sub = lane / kReduceCols;  // the two half-waves take alternate partial rows
+    const uint32_t c = blockIdx.x * kReduceCols + col;
     // 64-bit so that blocks near 2^32 cannot wrap the run length to zero.
     const uint64_t per = (static_cast<uint64_t>(blocks) + kReduceWaves - 1) / kReduceWaves;
     const uint32_t b0 = static_cast<uint32_t>(min(static_cast<uint64_t>(wave) * per, static_cast<uint64_t>(blocks)));
     const uint32_t b1 = static_cast<uint32_t>(min(static_cast<uint64_t>(b0) + per, static_cast<uint64_t>(blocks)));
     float sum = 0.0f;
     if (c < n) {
-        uint32_t b = b0;
-        for (; b + 8 <= b1; b += 8) {
+        uint32_t b = b0 + sub;
+        for (; b + 14 < b1; b += 16) {
             float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = dw_partial[static_cast<uint64_t>(b + u) * n + c];
+            for (int u = 0; u < 8; ++u) v[u] = dw_partial[static_cast<uint64_t>(b + 2 * u) * n + c];
 #pragma unroll
             for (int u = 0; u < 8; ++u) sum += v[u];
         }
-        for (; b < b1; ++b) sum += dw_partial[static_cast<uint64_t>(b) * n + c];
+        for (; b < b1; b += 2) sum += dw_partial[static_cast<uint64_t>(b) * n + c];
     }
-    run_sum[wave][lane] = sum;
+    sum += __shfl_xor(sum, kReduceCols, 64);
+    if (sub == 0) run_sum[wave][col] = sum;
     __syncthreads();
-    if (wave == 0 && c < n) {
+    if (wave == 0 && sub == 0 && c < n) {
         float total = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kReduceWaves; ++w) total += run_sum[w][lane];
+        for (int w = 0; w < kReduceWaves; ++w) total += run_sum[w][col];
         store_rn<W>(dw + c, total);
     }
 }
@@ -1062,7 +1068,7 @@ extern "C" int kcr_rms_norm_reduce_weight_grad(const kcr_tensor* dw, const kcr_t
         check_contiguous(dw, "dw");
         check_contiguous(dw_partial, "dw_partial");
         auto s = static_cast<hipStream_t>(stream);
-        const unsigned grid = static_cast<unsigned>((n + 63) / 64);
+        const unsigned grid = static_cast<unsigned>((n + kReduceCols - 1) / kReduceCols);
         constexpr unsigned threads = 64 * kReduceWaves;
         const auto* p = static_cast<const float*>(dw_partial->data);
         switch (dw->dtype) {
