@@ -645,6 +645,37 @@ __device__ __forceinline__ uint32_t keep_bits_query_lane_shared(const DropoutSta
     return bits;
 }
 
+// Zeroes the dropped entries of the 16 scores a lane holds for query q of the
+// 32-key block kblock (the S^T accumulator layout; element r is key
+// 8 (r / 4) + 4 hh + r % 4): the keep decisions of keep_bits_query_lane_shared,
+// applied directly. Of the two Philox words an element may come from, the lane
+// computed one and lane l ^ 8 (same row of 16) the other; a DPP row_ror:8 move
+// restricted to the banks (4-lane groups) that need the partner's word fetches
+// it, so each element costs one byte extract, one compare and one select.
+// Requires q % 16 == lane % 16.
+__device__ __forceinline__ void apply_dropout_query_lane(const DropoutState& d, uint32_t bh, uint32_t q,
+                                                         uint32_t kblock, int hh, f32x16& s) {
+    const uint32_t own_t = (q % 16u) / 8u;
+    uint32_t own[4];
+    philox4x32_7(d.seed, d.offset + 32ull * bh + 4u * (q % 8u) + 2u * hh + own_t, q / 16u, kblock, own);
+    const uint32_t rshift = own_t * 16u;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+        const int o = static_cast<int>(own[wi]);
+        // Word of counter t = 0: lanes 8-15 of each row (banks 2, 3) take lane l - 8's.
+        const uint32_t w0 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(o, o, 0x128, 0xF, 0xC, false));
+        // Word of counter t = 1: lanes 0-7 (banks 0, 1) take lane l + 8's.
+        const uint32_t w1 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(o, o, 0x128, 0xF, 0x3, false));
+        const uint32_t h0 = w0 >> rshift, h1 = w1 >> rshift;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int r0 = 4 * wi + e, r1 = 4 * wi + 2 + e;
+            s[r0] = ((h0 >> (8 * e)) & 255u) <= d.threshold ? s[r0] : 0.0f;
+            s[r1] = ((h1 >> (8 * e)) & 255u) <= d.threshold ? s[r1] : 0.0f;
+        }
+    }
+}
+
 // keep_bits_key_lane for a wave whose lane l holds key k with k % 32 == l % 32
 // (all 64 lanes active). The 8 Philox calls per lane above cover only 32
 // distinct counters per half-wave: (m, rb) x (k % 8) / 2. Lane 8j + 2c + e of a

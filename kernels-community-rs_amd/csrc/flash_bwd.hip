@@ -744,10 +744,10 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
                 float dsv[16];
-                uint32_t keep_bits = 0xFFFFu;
+                // Dropped entries of dP are zeroed (dS = P (dP M - delta)).
                 if constexpr (DROPOUT) {
-                    keep_bits = keep_bits_query_lane_shared(drop, bh, static_cast<uint32_t>(my_row),
-                                                     static_cast<uint32_t>(kb / 32 + sub), hh);
+                    apply_dropout_query_lane(drop, bh, static_cast<uint32_t>(my_row),
+                                             static_cast<uint32_t>(kb / 32 + sub), hh, dp[sub]);
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -758,7 +758,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
                                             (wl >= 0 & col < my_row + off - wl);
                         pr = masked ? 0.0f : pr;
                     }
-                    dsv[r] = pr * ((((keep_bits >> r) & 1u) ? dp[sub][r] : 0.0f) - dlt);
+                    dsv[r] = pr * (dp[sub][r] - dlt);
                 }
 #pragma unroll
                 for (int t2 = 0; t2 < 2; ++t2) {

@@ -703,10 +703,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
             // leave P (and O) only.
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
-                const uint32_t bits = keep_bits_query_lane_shared(drop, bh, static_cast<uint32_t>(row),
-                                                           static_cast<uint32_t>(kb / 32 + sub), hh);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) s[sub][r] = ((bits >> r) & 1u) ? s[sub][r] : 0.0f;
+                apply_dropout_query_lane(drop, bh, static_cast<uint32_t>(row), static_cast<uint32_t>(kb / 32 + sub),
+                                         hh, s[sub]);
             }
         }
         // P^T packed in place: k-slot j of group tt is key 16tt + 8(j/4) + 4hh + j%4.
