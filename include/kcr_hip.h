@@ -139,13 +139,28 @@ typedef struct kcr_dropout {
 
 /* Dense forward. replaces `fwd_lse(q,k,v,alibi,scale,causal,wl,wr,softcap,out)`
  * (flash-attn2-rs/src/host/forward/mod.rs:835-853; arities mod.rs:53-61) and `fwd`
- * (mod.rs:815-833); dropout as in mod.rs:73-199 (return_softmax excluded).
+ * (mod.rs:815-833); dropout as in mod.rs:73-199 (return_softmax: kcr_flash_fwd_softmax).
  *   q [B,Sq,H,D], k/v [B,Sk,Hk,D] fp16/bf16, last stride 1;
  *   out like q (written), lse float32 contiguous [B,H,Sq] (written). */
 int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
                   const kcr_tensor* alibi, int has_scale, double scale, int causal,
                   int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                   const kcr_tensor* out, const kcr_tensor* lse, void* stream);
+
+/* Dense forward with diagnostic probabilities. replaces `fwd` with arity 14 and
+ * return_softmax = true (flash-attn2-rs/src/host/forward/mod.rs:133-199, 382-398,
+ * 526-540; kernel write src/device/dropout.rs:93-112). Arguments as kcr_flash_fwd;
+ * dropout must have p > 0 and an rng_state tensor. probabilities: contiguous,
+ * q's dtype, [B, H, ceil128(Sq), ceil128(Sk)] (written in full): element (q, k)
+ * that the mask leaves visible holds exp(scale q.k + bias - lse), its sign bit
+ * set when dropout drops it; padding and masked elements are +0. (The
+ * reference's magnitudes carry the running maximum of its key tile instead of
+ * the final LSE; the sign pattern is the same.) */
+int kcr_flash_fwd_softmax(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                          const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                          int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
+                          const kcr_tensor* out, const kcr_tensor* lse, const kcr_tensor* probabilities,
+                          void* stream);
 
 /* Varlen forward. replaces the plain (non-paged, non-cached, p == 0) form of
  * `varlen_fwd_explicit(q,k,v,cuq,cuk,seqused_k,leftpad_k,alibi,scale,causal,
@@ -160,6 +175,20 @@ int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_ten
                          int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
                          int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors,
                          const kcr_tensor* out, const kcr_tensor* lse, void* stream);
+
+/* Varlen forward with diagnostic probabilities. replaces `varlen_fwd_explicit`
+ * with return_softmax = true (flash-attn2-rs/src/host/varlen/mod.rs:201-209,
+ * 400-455). Arguments as kcr_flash_varlen_fwd; probabilities as for
+ * kcr_flash_fwd_softmax with shape [B, H, ceil128(max_seqlen_q),
+ * ceil128(max_seqlen_k)], rows and columns local to sequence b. */
+int kcr_flash_varlen_fwd_softmax(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                                 const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
+                                 const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
+                                 const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                                 int64_t window_left, int64_t window_right, double softcap,
+                                 const kcr_dropout* dropout, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                 int zero_tensors, const kcr_tensor* out, const kcr_tensor* lse,
+                                 const kcr_tensor* probabilities, void* stream);
 
 /* KV-cache append. replaces `cache_update_explicit(q, kcache, vcache, k, v, lengths,
  * cos, sin, indices, table, interleaved, advance_q)` (flash-attn2-rs/src/host/cache/

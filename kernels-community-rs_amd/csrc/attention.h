@@ -741,6 +741,13 @@ private:
     hipStream_t stream_;
 };
 
+// Diagnostic probabilities of a dropout forward (flash_probs.hip): fills the
+// whole [batch, heads, rq, rk] plane `probs` (q's dtype, contiguous, rq and rk
+// multiples of 128) from the inputs, masks, dropout state and the LSE the
+// forward in `prm` wrote.
+void launch_dropout_probabilities(const FwdParams& prm, bool varlen, int dtype, void* probs, int64_t rq,
+                                  int64_t rk, hipStream_t s);
+
 // Whether two tensors' byte ranges intersect.
 bool spans_overlap(const kcr_tensor* a, const kcr_tensor* b);
 

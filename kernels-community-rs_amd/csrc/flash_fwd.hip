@@ -1348,14 +1348,34 @@ namespace {
 void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* alibi,
                    int32_t alibi_b, const Options& opt, const DropoutArgs& drop, int64_t B, int64_t Sq,
                    int64_t H, int64_t D, int64_t Sk, int64_t Hk, const kcr_tensor* out,
-                   const kcr_tensor* lse, hipStream_t s);
-}  // namespace
+                   const kcr_tensor* lse, const kcr_tensor* probs, hipStream_t s);
 
-extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
-                             const kcr_tensor* alibi, int has_scale, double scale, int causal,
-                             int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
-                             const kcr_tensor* out, const kcr_tensor* lse, void* stream) {
-    return guarded([&] {
+int64_t round128(int64_t n) { return (n + 127) / 128 * 128; }
+
+// The diagnostic-probability output of a forward with return_softmax
+// (host/forward/mod.rs:181-199, 382-398; host/varlen/mod.rs:201-209, 400-414):
+// dropout with an RNG-state tensor, and a contiguous [batch, H, ceil128(Sq),
+// ceil128(Sk)] tensor of q's dtype.
+void check_probabilities(const kcr_tensor* probs, const kcr_dropout* dropout, const DropoutArgs& drop,
+                         const kcr_tensor* q, int64_t batch, int64_t H, int64_t Sq, int64_t Sk) {
+    if (drop.threshold >= 255 || !dropout || !dropout->rng_state) {
+        throw value_error("return_softmax requires nonzero dropout and a CUDA RNG-state tensor");
+    }
+    if (!probs || probs->dtype != q->dtype || probs->ndim != 4 || probs->shape[0] != batch ||
+        probs->shape[1] != H || probs->shape[2] != round128(Sq) || probs->shape[3] != round128(Sk) ||
+        !is_contiguous(*probs) || reinterpret_cast<uintptr_t>(probs->data) % 8 != 0) {
+        throw value_error("probabilities must be a contiguous tensor of q's dtype with shape [" +
+                          std::to_string(batch) + ", " + std::to_string(H) + ", " +
+                          std::to_string(round128(Sq)) + ", " + std::to_string(round128(Sk)) + "]");
+    }
+    require_device(probs, "probabilities");
+}
+
+void dense_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* alibi,
+                    int has_scale, double scale, int causal, int64_t window_left, int64_t window_right,
+                    double softcap, const kcr_dropout* dropout, const kcr_tensor* out, const kcr_tensor* lse,
+                    const kcr_tensor* probs, void* stream) {
+    {
         check_qkv(q, "q", 4);
         check_qkv(k, "k", 4);
         check_qkv(v, "v", 4);
@@ -1403,6 +1423,7 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         const Options opt = normalize_options(has_scale, scale, causal, window_left, window_right,
                                               softcap, D, Sk);
         const DropoutArgs drop = parse_dropout(dropout, softcap, q);
+        if (probs) check_probabilities(probs, dropout, drop, q, B, H, Sq, Sk);
         if (Sq == 0) return;
         // Packed copies of inputs the tile loads cannot read, and of an output
         // they cannot write or that overlaps an input (host/layout.rs:46-125,
@@ -1413,8 +1434,31 @@ extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         k = sk_.get();
         v = sv_.get();
         out = so_.get();
-        run_dense_fwd(q, k, v, alibi, alibi_b, opt, drop, B, Sq, H, D, Sk, Hk, out, lse, s);
+        run_dense_fwd(q, k, v, alibi, alibi_b, opt, drop, B, Sq, H, D, Sk, Hk, out, lse, probs, s);
         so_.copy_out();
+    }
+}
+}  // namespace
+
+extern "C" int kcr_flash_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                             const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                             int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
+                             const kcr_tensor* out, const kcr_tensor* lse, void* stream) {
+    return guarded([&] {
+        dense_fwd_impl(q, k, v, alibi, has_scale, scale, causal, window_left, window_right, softcap, dropout,
+                       out, lse, nullptr, stream);
+    });
+}
+
+extern "C" int kcr_flash_fwd_softmax(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                                     const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                                     int64_t window_left, int64_t window_right, double softcap,
+                                     const kcr_dropout* dropout, const kcr_tensor* out, const kcr_tensor* lse,
+                                     const kcr_tensor* probabilities, void* stream) {
+    return guarded([&] {
+        if (!probabilities) throw value_error("probabilities is required");
+        dense_fwd_impl(q, k, v, alibi, has_scale, scale, causal, window_left, window_right, softcap, dropout,
+                       out, lse, probabilities, stream);
     });
 }
 
@@ -1458,7 +1502,7 @@ int64_t dense_splits(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int cus) {
 void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v, const kcr_tensor* alibi,
                    int32_t alibi_b, const Options& opt, const DropoutArgs& drop, int64_t B, int64_t Sq,
                    int64_t H, int64_t D, int64_t Sk, int64_t Hk, const kcr_tensor* out,
-                   const kcr_tensor* lse, hipStream_t s) {
+                   const kcr_tensor* lse, const kcr_tensor* probs, hipStream_t s) {
     {
         if (Sk == 0) {
             // Every row is empty: O = 0, LSE = +inf.
@@ -1504,8 +1548,13 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
         const int64_t splits = (general || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
                                    ? 1
                                    : dense_splits(B, H, Sq, Sk, compute_units());
+        // The probabilities read the final LSE (after any merge).
+        auto probabilities = [&] {
+            if (probs) launch_dropout_probabilities(prm, false, q->dtype, probs->data, round128(Sq), round128(Sk), s);
+        };
         if (splits <= 1) {
             launch_fwd<false>(prm, q->dtype, bucket, general, s);
+            probabilities();
             return;
         }
         // Key splits for an underfilled grid (host/forward/dispatch.rs:127-238
@@ -1522,20 +1571,20 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
         launch_fwd<false>(prm, q->dtype, bucket, false, s);
         launch_merge(prm, q->dtype, bucket, static_cast<int>(Sq), s);
         check_hip(hipFreeAsync(ws, s), "hipFreeAsync (split partials)");
+        probabilities();
     }
 }
 
 }  // namespace
 
-extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
-                                    const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
-                                    const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
-                                    const kcr_tensor* alibi, int has_scale, double scale,
-                                    int causal, int64_t window_left, int64_t window_right,
-                                    double softcap, const kcr_dropout* dropout, int64_t max_seqlen_q, int64_t max_seqlen_k,
-                                    int zero_tensors, const kcr_tensor* out,
-                                    const kcr_tensor* lse, void* stream) {
-    return guarded([&] {
+namespace {
+void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                     const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k, const kcr_tensor* seqused_k,
+                     const kcr_tensor* leftpad_k, const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                     int64_t window_left, int64_t window_right, double softcap, const kcr_dropout* dropout,
+                     int64_t max_seqlen_q, int64_t max_seqlen_k, int zero_tensors, const kcr_tensor* out,
+                     const kcr_tensor* lse, const kcr_tensor* probs, void* stream) {
+    {
         check_qkv(q, "q", 3);
         check_qkv(k, "k", 3);
         check_qkv(v, "v", 3);
@@ -1588,6 +1637,7 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
         const Options opt = normalize_options(has_scale, scale, causal_eff, window_left, window_right,
                                               softcap, D, max_seqlen_k);
         const DropoutArgs drop = parse_dropout(dropout, softcap, q);
+        if (probs) check_probabilities(probs, dropout, drop, q, batch, H, max_seqlen_q, max_seqlen_k);
         // Packed copies of what the tile loads cannot use (host/layout.rs:46-125).
         Staged sq_(q, s, true), sk_(k, s, true, 0, D), sv_(v, s, true, 0, D);
         Staged so_(out, s, zero_tensors == 0, -1, 0, {q, k, v});
@@ -1603,6 +1653,11 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
             fill_f32(static_cast<float*>(lse->data), H * Tq, max_seqlen_k == 0 ? INFINITY : -INFINITY, s);
         }
         if (Tq == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) {
+            // No sequence row: the probability plane is all zero (varlen/mod.rs:445-455).
+            if (probs) {
+                fill_f32(static_cast<float*>(probs->data),
+                         batch * H * round128(max_seqlen_q) * round128(max_seqlen_k) / 2, 0.0f, s);
+            }
             so_.copy_out();
             return;
         }
@@ -1661,7 +1716,43 @@ extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, co
             launch_merge(prm, q->dtype, bucket, static_cast<int>(Tq), s);
             check_hip(hipFreeAsync(ws, s), "hipFreeAsync (split partials)");
         }
+        if (probs) {
+            launch_dropout_probabilities(prm, true, q->dtype, probs->data, round128(max_seqlen_q),
+                                         round128(max_seqlen_k), s);
+        }
         so_.copy_out();
+    }
+}
+}  // namespace
+
+extern "C" int kcr_flash_varlen_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                                    const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
+                                    const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
+                                    const kcr_tensor* alibi, int has_scale, double scale,
+                                    int causal, int64_t window_left, int64_t window_right,
+                                    double softcap, const kcr_dropout* dropout, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                    int zero_tensors, const kcr_tensor* out,
+                                    const kcr_tensor* lse, void* stream) {
+    return guarded([&] {
+        varlen_fwd_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi, has_scale, scale, causal,
+                        window_left, window_right, softcap, dropout, max_seqlen_q, max_seqlen_k, zero_tensors, out,
+                        lse, nullptr, stream);
+    });
+}
+
+extern "C" int kcr_flash_varlen_fwd_softmax(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v,
+                                            const kcr_tensor* cu_seqlens_q, const kcr_tensor* cu_seqlens_k,
+                                            const kcr_tensor* seqused_k, const kcr_tensor* leftpad_k,
+                                            const kcr_tensor* alibi, int has_scale, double scale, int causal,
+                                            int64_t window_left, int64_t window_right, double softcap,
+                                            const kcr_dropout* dropout, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                                            int zero_tensors, const kcr_tensor* out, const kcr_tensor* lse,
+                                            const kcr_tensor* probabilities, void* stream) {
+    return guarded([&] {
+        if (!probabilities) throw value_error("probabilities is required");
+        varlen_fwd_impl(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi, has_scale, scale, causal,
+                        window_left, window_right, softcap, dropout, max_seqlen_q, max_seqlen_k, zero_tensors, out,
+                        lse, probabilities, stream);
     });
 }
 

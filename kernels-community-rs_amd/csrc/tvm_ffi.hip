@@ -457,14 +457,15 @@ namespace ffi {
 namespace {
 
 // fwd / fwd_lse (host/forward/mod.rs:52-61, 815-853): 9 base arguments, then
-// optionally (p, seed | state, offset) and/or the output tensor.
+// optionally (p, seed | state, offset) and/or the output tensor; arity 14 is
+// (..., p, state, offset, out | None, return_softmax) and returns
+// [out, lse, probabilities] (mod.rs:133-199, 382-398).
 void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
     const int n = a.n;
-    if (n == 14 || n == 16 || n == 18) {
-        throw runtime_error("diagnostic probabilities and generator descriptors (fwd arities 14/16/18) are "
-                            "not part of this build");
+    if (n == 16 || n == 18) {
+        throw runtime_error("generator-descriptor RNG reservation (fwd arities 16/18) is not part of this build");
     }
-    if (n != 9 && n != 10 && n != 12 && n != 13) {
+    if (n != 9 && n != 10 && n != 12 && n != 13 && n != 14) {
         throw value_error("fwd expects 9 positional arguments (q, k, v, alibi_slopes, softmax_scale, is_causal, "
                           "window_size_left, window_size_right, softcap), optionally followed by p_dropout, "
                           "seed, offset, and/or an output tensor; got " +
@@ -472,24 +473,43 @@ void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
     }
     const DLTensor* q = a.dltensor(0);
     if (q->ndim != 4) throw value_error("q must have 4 dimensions [B, S, H, D]");
-    const bool supplied = n == 10 || n == 13;
+    const int out_idx = n == 14 ? 12 : n - 1;
+    const bool supplied = n == 10 || n == 13 || (n == 14 && !a.none(12));
+    const bool return_softmax = n == 14 && a.boolean(13);
     if (lse_only && !supplied) throw value_error("LSE-only forward requires a supplied output");
+    if (lse_only && return_softmax) throw value_error("LSE-only forward cannot return diagnostic probabilities");
     const Drop drop = n >= 12 ? dropout_of(a, 9, 10, 11, false) : Drop{};
+    if (return_softmax && (!drop.on || !drop.d.rng_state)) {
+        throw value_error("return_softmax requires nonzero dropout and a CUDA RNG-state tensor");
+    }
     int has_scale;
     double scale;
     scale_of(a, 4, has_scale, scale);
     const View vq = view_of(q, a.op), vk = view_of(a.dltensor(1), a.op), vv = view_of(a.dltensor(2), a.op),
                al = view_of(a.opt_dltensor(3), a.op);
     Owned out_o;
-    const DLTensor* out = supplied ? a.dltensor(n - 1) : nullptr;
+    const DLTensor* out = supplied ? a.dltensor(out_idx) : nullptr;
     if (!supplied) {
         out_o = alloc({q->shape[0], q->shape[1], q->shape[2], q->shape[3]}, q->dtype, q->device);
         out = out_o.dl;
     }
     Owned lse = alloc({q->shape[0], q->shape[2], q->shape[1]}, kF32, q->device);
     const View vo = view_of(out, a.op), vl = view_of(lse.dl, a.op);
-    check_status(kcr_flash_fwd(vq.ptr(), vk.ptr(), vv.ptr(), al.ptr(), has_scale, scale, a.boolean(5) ? 1 : 0,
-                               a.i64(6), a.i64(7), a.f64(8), drop.ptr(), vo.ptr(), vl.ptr(), stream_for(q)));
+    Owned probs;
+    if (return_softmax) {
+        const auto round128 = [](int64_t x) { return (x + 127) / 128 * 128; };
+        probs = alloc({q->shape[0], q->shape[2], round128(q->shape[1]), round128(a.dltensor(1)->shape[1])},
+                      q->dtype, q->device);
+        const View vp = view_of(probs.dl, a.op);
+        check_status(kcr_flash_fwd_softmax(vq.ptr(), vk.ptr(), vv.ptr(), al.ptr(), has_scale, scale,
+                                           a.boolean(5) ? 1 : 0, a.i64(6), a.i64(7), a.f64(8), drop.ptr(),
+                                           vo.ptr(), vl.ptr(), vp.ptr(), stream_for(q)));
+    } else {
+        check_status(kcr_flash_fwd(vq.ptr(), vk.ptr(), vv.ptr(), al.ptr(), has_scale, scale,
+                                   a.boolean(5) ? 1 : 0, a.i64(6), a.i64(7), a.f64(8), drop.ptr(), vo.ptr(),
+                                   vl.ptr(), stream_for(q)));
+        if (n == 14) probs = alloc({0}, q->dtype, q->device);
+    }
     if (lse_only) {
         set_tensor(r, lse);
         return;
@@ -498,19 +518,20 @@ void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
     if (supplied) {
         // The supplied output is the caller's tensor: the array needs it as an
         // owned object only when it was passed as one.
-        if (a.at(n - 1).type_index != kTensor) {
+        if (a.at(out_idx).type_index != kTensor) {
             throw runtime_error("fwd with a supplied output returns [out, lse] and needs `out` as a Tensor object");
         }
         const auto inc = runtime_fn<int (*)(void*)>("TVMFFIObjectIncRef");
         if (!inc) throw runtime_error("returning an Array needs the tvm-ffi runtime (TVMFFIObjectIncRef)");
         Owned o;
-        o.handle = a.at(n - 1).v_ptr;
+        o.handle = a.at(out_idx).v_ptr;
         inc(o.handle);
         items.push_back(std::move(o));
     } else {
         items.push_back(std::move(out_o));
     }
     items.push_back(std::move(lse));
+    if (n == 14) items.push_back(std::move(probs));
     set_array(r, items);
 }
 
@@ -628,9 +649,6 @@ extern "C" int32_t __tvm_ffi_varlen_fwd_explicit(void*, const TVMFFIAny* args, i
             (a.boolean(17) && !(static_cast<float>(p) > 0.0f))) {
             throw kcr::value_error("invalid dropout, softcap, or probability request");
         }
-        if (a.boolean(17)) {
-            throw kcr::runtime_error("diagnostic probabilities (return_softmax) are not part of this build");
-        }
         kcr::ffi::Drop drop;
         if (static_cast<float>(p) > 0.0f) {
             if (a.none(14)) throw kcr::value_error("dropout requires RNG state");
@@ -641,16 +659,34 @@ extern "C" int32_t __tvm_ffi_varlen_fwd_explicit(void*, const TVMFFIAny* args, i
         kcr::ffi::scale_of(a, 8, has_scale, scale);
         Owned out = kcr::ffi::alloc({q->shape[0], q->shape[1], q->shape[2]}, q->dtype, q->device);
         Owned lse = kcr::ffi::alloc({q->shape[1], q->shape[0]}, kcr::ffi::kF32, q->device);
-        Owned probs = kcr::ffi::alloc({0}, q->dtype, q->device);
+        const bool return_softmax = a.boolean(17);
+        if (return_softmax && (a.dltensor(3)->ndim != 1 || a.dltensor(3)->shape[0] < 2 || a.i64(15) < 0 ||
+                               a.i64(16) < 0 || a.i64(15) > INT32_MAX - 256 || a.i64(16) > INT32_MAX - 256)) {
+            throw kcr::value_error("unsupported packed attention dimensions");
+        }
+        const auto round128 = [](int64_t x) { return (x + 127) / 128 * 128; };
+        Owned probs = return_softmax
+                          ? kcr::ffi::alloc({a.dltensor(3)->shape[0] - 1, q->shape[1], round128(a.i64(15)),
+                                             round128(a.i64(16))},
+                                            q->dtype, q->device)
+                          : kcr::ffi::alloc({0}, q->dtype, q->device);
         const View vq = kcr::ffi::view_of(q, a.op), vk = kcr::ffi::view_of(a.dltensor(1), a.op),
                    vv = kcr::ffi::view_of(a.dltensor(2), a.op), cq = kcr::ffi::view_of(a.dltensor(3), a.op),
                    ck = kcr::ffi::view_of(a.dltensor(4), a.op), su = kcr::ffi::view_of(a.opt_dltensor(5), a.op),
                    lp = kcr::ffi::view_of(a.opt_dltensor(6), a.op), al = kcr::ffi::view_of(a.opt_dltensor(7), a.op),
                    vo = kcr::ffi::view_of(out.dl, a.op), vl = kcr::ffi::view_of(lse.dl, a.op);
-        kcr::ffi::check_status(kcr_flash_varlen_fwd(
-            vq.ptr(), vk.ptr(), vv.ptr(), cq.ptr(), ck.ptr(), su.ptr(), lp.ptr(), al.ptr(), has_scale, scale,
-            a.boolean(9) ? 1 : 0, a.i64(10), a.i64(11), a.f64(12), drop.ptr(), a.i64(15), a.i64(16),
-            a.boolean(18) ? 1 : 0, vo.ptr(), vl.ptr(), kcr::ffi::stream_for(q)));
+        if (return_softmax) {
+            const View vp = kcr::ffi::view_of(probs.dl, a.op);
+            kcr::ffi::check_status(kcr_flash_varlen_fwd_softmax(
+                vq.ptr(), vk.ptr(), vv.ptr(), cq.ptr(), ck.ptr(), su.ptr(), lp.ptr(), al.ptr(), has_scale, scale,
+                a.boolean(9) ? 1 : 0, a.i64(10), a.i64(11), a.f64(12), drop.ptr(), a.i64(15), a.i64(16),
+                a.boolean(18) ? 1 : 0, vo.ptr(), vl.ptr(), vp.ptr(), kcr::ffi::stream_for(q)));
+        } else {
+            kcr::ffi::check_status(kcr_flash_varlen_fwd(
+                vq.ptr(), vk.ptr(), vv.ptr(), cq.ptr(), ck.ptr(), su.ptr(), lp.ptr(), al.ptr(), has_scale, scale,
+                a.boolean(9) ? 1 : 0, a.i64(10), a.i64(11), a.f64(12), drop.ptr(), a.i64(15), a.i64(16),
+                a.boolean(18) ? 1 : 0, vo.ptr(), vl.ptr(), kcr::ffi::stream_for(q)));
+        }
         std::vector<Owned> items;
         items.push_back(std::move(out));
         items.push_back(std::move(lse));

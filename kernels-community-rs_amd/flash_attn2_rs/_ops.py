@@ -3,6 +3,8 @@ positional signatures and return conventions, backed by libkcr_hip.so.
 
   fwd(q, k, v, alibi, scale, causal, wl, wr, softcap[, p, seed, offset][, out])
       -> [out, lse]                          host/forward/mod.rs:52-61, 815-833
+  fwd(..., p, state, offset, out, return_softmax)
+      -> [out, lse, probabilities]           host/forward/mod.rs:133-199, 382-398
   fwd_lse(..., out) -> lse                   host/forward/mod.rs:835-853
   varlen_fwd_explicit(q, k, v, cuq, cuk, seqused_k, leftpad_k, alibi, scale, causal,
       left, right, softcap, p, state, max_q, max_k, return_softmax, zero_tensors)
@@ -26,8 +28,9 @@ torch's allocator (the same allocator tvm-ffi forwards to under torch). Inputs
 whose rows are not 16-byte aligned are repacked first, as the reference does
 with `copy_attention_layout` (host/layout.rs:46-125). Dropout follows the
 reference's Philox4x32-7 mask stream, keyed by explicit (seed, offset) or by a
-device int64 [2] RNG-state tensor; diagnostic probabilities (return_softmax) and
-the generator-descriptor arities are not part of this build.
+device int64 [2] RNG-state tensor. Diagnostic probabilities (return_softmax)
+come from kcr_flash_fwd_softmax / kcr_flash_varlen_fwd_softmax; the
+generator-descriptor arities (16 and 18) are not part of this build.
 """
 
 from __future__ import annotations
@@ -74,17 +77,20 @@ def _rng_state_ok(state, q):
             and state.data_ptr() % 8 == 0)
 
 
+def _round128(n):
+    return (int(n) + 127) // 128 * 128
+
+
 def _scale_args(scale):
     return (0, ctypes.c_double(0.0)) if scale is None else (1, ctypes.c_double(float(scale)))
 
 
 def _fwd_impl(args, lse_only):
     n = len(args)
-    if n in (14, 16, 18):
+    if n in (16, 18):
         raise NotImplementedError(
-            "diagnostic probabilities and generator descriptors (fwd arities 14/16/18) are not "
-            "part of this build")
-    if n not in (9, 10, 12, 13):
+            "generator-descriptor RNG reservation (fwd arities 16/18) is not part of this build")
+    if n not in (9, 10, 12, 13, 14):
         raise ValueError(
             "fwd expects 9 positional arguments (q, k, v, alibi_slopes, softmax_scale, "
             "is_causal, window_size_left, window_size_right, softcap), optionally followed by "
@@ -99,9 +105,14 @@ def _fwd_impl(args, lse_only):
         else:
             seed = int(args[10])
         offset = int(args[11])
-    supplied = args[-1] if n in (10, 13) else None
+    return_softmax = n == 14 and bool(args[13])
+    supplied = args[12] if n == 14 else args[-1] if n in (10, 13) else None
     if lse_only and supplied is None:
         raise ValueError("LSE-only forward requires a supplied output")
+    if lse_only and return_softmax:
+        raise ValueError("LSE-only forward cannot return diagnostic probabilities")
+    if return_softmax and (float(np.float32(p)) == 0.0 or state is None):
+        raise ValueError("return_softmax requires nonzero dropout and a CUDA RNG-state tensor")
     if q.ndim != 4:
         raise ValueError(f"q must have 4 dimensions [B, S, H, D], got shape {list(q.shape)}")
     b, sq, h, d = q.shape
@@ -113,10 +124,21 @@ def _fwd_impl(args, lse_only):
     has_scale, sc = _scale_args(scale)
     descs = [describe(t) for t in (q, k, v, alibi)]
     keep_alive, drop = dropout_arg(p, seed, offset, state)
-    call("kcr_flash_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
-         ctypes.c_int64(int(wl)), ctypes.c_int64(int(wr)), ctypes.c_double(float(softcap)), drop,
-         ref(describe(out)), ref(describe(lse)), stream_of(q))
-    return lse if lse_only else [out, lse]
+    scalars = (has_scale, sc, int(bool(causal)), ctypes.c_int64(int(wl)), ctypes.c_int64(int(wr)),
+               ctypes.c_double(float(softcap)), drop)
+    if return_softmax:
+        sk = k.shape[1]
+        probabilities = torch.empty((b, h, _round128(sq), _round128(sk)), dtype=q.dtype, device=q.device)
+        call("kcr_flash_fwd_softmax", *(ref(x) for x in descs), *scalars, ref(describe(out)),
+             ref(describe(lse)), ref(describe(probabilities)), stream_of(q))
+        return [out, lse, probabilities]
+    call("kcr_flash_fwd", *(ref(x) for x in descs), *scalars, ref(describe(out)), ref(describe(lse)),
+         stream_of(q))
+    if lse_only:
+        return lse
+    if n == 14:
+        return [out, lse, torch.empty(0, dtype=q.dtype, device=q.device)]
+    return [out, lse]
 
 
 def fwd(*args):
@@ -139,8 +161,6 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
             or (float(np.float32(p)) > 0.0 and float(softcap) > 0.0)
             or (return_softmax and float(np.float32(p)) == 0.0)):
         raise ValueError("invalid dropout, softcap, or probability request")
-    if return_softmax:
-        raise NotImplementedError("diagnostic probabilities (return_softmax) are not part of this build")
     if float(np.float32(p)) > 0.0:
         if state is None:
             raise ValueError("dropout requires RNG state")
@@ -158,11 +178,18 @@ def varlen_fwd_explicit(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_
     has_scale, sc = _scale_args(scale)
     descs = [describe(t) for t in (q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi)]
     keep_alive, drop = dropout_arg(p, 0, 0, state)
-    call("kcr_flash_varlen_fwd", *(ref(x) for x in descs), has_scale, sc, int(bool(causal)),
-         ctypes.c_int64(int(left)), ctypes.c_int64(int(right)), ctypes.c_double(float(softcap)), drop,
-         ctypes.c_int64(int(max_q)), ctypes.c_int64(int(max_k)), int(bool(zero_tensors)),
-         ref(describe(out)), ref(describe(lse)), stream_of(q))
-    probabilities = torch.empty(0, dtype=q.dtype, device=q.device)
+    scalars = (has_scale, sc, int(bool(causal)), ctypes.c_int64(int(left)), ctypes.c_int64(int(right)),
+               ctypes.c_double(float(softcap)), drop, ctypes.c_int64(int(max_q)), ctypes.c_int64(int(max_k)),
+               int(bool(zero_tensors)))
+    if return_softmax:
+        probabilities = torch.empty((batch, h, _round128(max_q), _round128(max_k)), dtype=q.dtype,
+                                    device=q.device)
+        call("kcr_flash_varlen_fwd_softmax", *(ref(x) for x in descs), *scalars, ref(describe(out)),
+             ref(describe(lse)), ref(describe(probabilities)), stream_of(q))
+    else:
+        probabilities = torch.empty(0, dtype=q.dtype, device=q.device)
+        call("kcr_flash_varlen_fwd", *(ref(x) for x in descs), *scalars, ref(describe(out)),
+             ref(describe(lse)), stream_of(q))
     return [out, lse, probabilities]
 
 

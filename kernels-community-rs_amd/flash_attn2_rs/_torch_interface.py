@@ -22,17 +22,23 @@ def _custom_op(name):
 @_custom_op("_dense_forward")
 def _dense_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
                    left: int, right: int, softcap: float, slopes: Optional[torch.Tensor],
-                   dropout_p: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    out, lse, _, rng_state = fwd(q, k, v, alibi_slopes=slopes, p_dropout=dropout_p, softmax_scale=scale,
-                                 is_causal=causal, window_size_left=left, window_size_right=right,
-                                 softcap=softcap)
-    return out, lse, rng_state
+                   dropout_p: float, return_probs: bool
+                   ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    out, lse, probs, rng_state = fwd(q, k, v, alibi_slopes=slopes, p_dropout=dropout_p, softmax_scale=scale,
+                                     is_causal=causal, window_size_left=left, window_size_right=right,
+                                     softcap=softcap, return_softmax=return_probs)
+    return out, lse, probs, rng_state
+
+
+def _round128(n):
+    return (n + 127) // 128 * 128
 
 
 @_dense_forward.register_fake
-def _(q, k, v, scale, causal, left, right, softcap, slopes, dropout_p):
+def _(q, k, v, scale, causal, left, right, softcap, slopes, dropout_p, return_probs):
     b, sq, h, _ = q.shape
-    return (torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32),
+    p_shape = (b, h, _round128(sq), _round128(k.shape[1])) if return_probs else (0,)
+    return (torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32), q.new_empty(p_shape),
             q.new_empty((2,), dtype=torch.int64))
 
 
@@ -81,15 +87,16 @@ class _DenseAttention(torch.autograd.Function):
         scale = dim ** -0.5 if softmax_scale is None else float(softmax_scale)
         q, k, v = _pad(dim, q, k, v)
         left, right = window_size
-        out, lse, rng_state = _dense_forward(q, k, v, scale, bool(causal), int(left), int(right),
-                                             float(softcap), alibi_slopes, float(dropout_p))
+        out, lse, probs, rng_state = _dense_forward(q, k, v, scale, bool(causal), int(left), int(right),
+                                                    float(softcap), alibi_slopes, float(dropout_p),
+                                                    bool(return_attn_probs and float(dropout_p) > 0))
         ctx.save_for_backward(q, k, v, out, lse, alibi_slopes, rng_state)
         ctx.options = (scale, bool(causal), int(left), int(right), float(softcap), bool(deterministic),
                        float(dropout_p))
         ctx.dim, ctx.packing = dim, packing
         out = out[..., :dim]
         if return_attn_probs:
-            return out, lse, torch.empty(0, device=q.device, dtype=q.dtype)
+            return out, lse, probs
         return out
 
     @staticmethod
@@ -115,18 +122,21 @@ class _DenseAttention(torch.autograd.Function):
 def _varlen_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cuq: torch.Tensor,
                     cuk: torch.Tensor, max_q: int, max_k: int, scale: float, causal: bool,
                     left: int, right: int, softcap: float, slopes: Optional[torch.Tensor],
-                    dropout_p: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    out, lse, _, rng_state = varlen_fwd(q, k, v, cuq, cuk, max_seqlen_q=max_q, max_seqlen_k=max_k,
-                                        p_dropout=dropout_p, softmax_scale=scale, is_causal=causal,
-                                        window_size_left=left, window_size_right=right,
-                                        softcap=softcap, alibi_slopes=slopes)
-    return out, lse, rng_state
+                    dropout_p: float, return_probs: bool
+                    ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    out, lse, probs, rng_state = varlen_fwd(q, k, v, cuq, cuk, max_seqlen_q=max_q, max_seqlen_k=max_k,
+                                            p_dropout=dropout_p, softmax_scale=scale, is_causal=causal,
+                                            window_size_left=left, window_size_right=right,
+                                            softcap=softcap, alibi_slopes=slopes, return_softmax=return_probs)
+    return out, lse, probs, rng_state
 
 
 @_varlen_forward.register_fake
-def _(q, k, v, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes, dropout_p):
+def _(q, k, v, cuq, cuk, max_q, max_k, scale, causal, left, right, softcap, slopes, dropout_p,
+      return_probs):
     total, h, _ = q.shape
-    return (torch.empty_like(q), q.new_empty((h, total), dtype=torch.float32),
+    p_shape = (cuq.shape[0] - 1, h, _round128(max_q), _round128(max_k)) if return_probs else (0,)
+    return (torch.empty_like(q), q.new_empty((h, total), dtype=torch.float32), q.new_empty(p_shape),
             q.new_empty((2,), dtype=torch.int64))
 
 
@@ -186,16 +196,17 @@ class _VarlenAttention(torch.autograd.Function):
         scale = dim ** -0.5 if softmax_scale is None else float(softmax_scale)
         q, k, v = _pad(dim, q, k, v)
         left, right = window_size
-        out, lse, rng_state = _varlen_forward(q, k, v, cuq, cuk, int(max_q), int(max_k), scale,
-                                              bool(causal), int(left), int(right), float(softcap),
-                                              slopes, float(dropout_p))
+        out, lse, probs, rng_state = _varlen_forward(q, k, v, cuq, cuk, int(max_q), int(max_k), scale,
+                                                     bool(causal), int(left), int(right), float(softcap),
+                                                     slopes, float(dropout_p),
+                                                     bool(return_probs and float(dropout_p) > 0))
         ctx.save_for_backward(q, k, v, out, lse, cuq, cuk, slopes, rng_state)
         ctx.options = (int(max_q), int(max_k), scale, bool(causal), int(left), int(right), float(softcap),
                        float(dropout_p))
         ctx.dim, ctx.packing = dim, packing
         out = out[..., :dim]
         if return_probs:
-            return out, lse, torch.empty(0, device=q.device, dtype=q.dtype)
+            return out, lse, probs
         return out
 
     @staticmethod

@@ -15,8 +15,9 @@ backward. The reference reserves those values with
 `torch.Generator.philox_state` (Torch >= 2.14); this build draws them from the
 generator with `torch.randint`, so the stream is reproducible under
 `torch.manual_seed`, and a caller that passes the same [seed, offset] gets the
-reference's masks. Diagnostic probabilities (return_softmax), paged K/V and the
-KV-cache entry points are outside this build and raise NotImplementedError.
+reference's masks. With return_softmax the forward also returns the diagnostic
+probabilities [B, H, ceil128(Sq), ceil128(Sk)]: the softmax probability of each
+visible element, its sign bit set where dropout drops it.
 """
 
 from __future__ import annotations
@@ -53,8 +54,6 @@ def _new_rng_state(q, gen=None):
 def _check_return_softmax(return_softmax, p):
     if return_softmax and p == 0:
         raise RuntimeError("return_softmax is only supported when p_dropout > 0.0")
-    if return_softmax:
-        raise NotImplementedError("diagnostic probabilities (return_softmax) are not part of this build")
 
 
 def _validate(q, k, v, out, alibi, softcap, *, packed=False):
@@ -114,13 +113,16 @@ def fwd(q, k, v, out=None, alibi_slopes=None, p_dropout=0.0, softmax_scale=None,
         out = torch.empty_like(q)
     args = (q, k, v, alibi_slopes, float(softmax_scale), bool(is_causal), int(window_size_left),
             int(window_size_right), float(softcap))
+    probabilities = torch.empty(0, device=q.device, dtype=q.dtype)
     if p > 0:
         state = _new_rng_state(q, gen)
-        lse = ops.fwd_lse(*args, p, state, 0, out)
+        if return_softmax:
+            _, lse, probabilities = ops.fwd(*args, p, state, 0, out, True)
+        else:
+            lse = ops.fwd_lse(*args, p, state, 0, out)
     else:
         state = torch.empty(2, device=q.device, dtype=torch.int64)
         lse = ops.fwd_lse(*args, out)
-    probabilities = torch.empty(0, device=q.device, dtype=q.dtype)
     return [out, lse, probabilities, state]
 
 

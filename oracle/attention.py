@@ -134,6 +134,36 @@ def backward(q, k, v, out, dout, lse, *, softmax_scale=None, causal=False, windo
             np.transpose(dv, (0, 2, 1, 3)).astype(dtype), (keep * delta).astype(dtype))
 
 
+def probabilities(q, k, keep_mask, *, softmax_scale=None, causal=False, window_left=-1, window_right=-1,
+                  alibi_slopes=None, dtype=np.float32):
+    """Diagnostic probabilities of a dropout forward (return_softmax): float32
+    [B, H, ceil128(Sq), ceil128(Sk)]. Element (q, k) the mask leaves visible holds
+    P = exp(score - lse), negated (sign bit set, -0.0 for P = 0) where keep_mask
+    [B, H, Sq, Sk] is False; padding and masked elements are +0. The reference
+    encodes the drop decision in the same sign bit (src/device/dropout.rs:93-112,
+    host/forward/mod.rs:382-398); its magnitudes are scaled by the running row
+    maximum of its key tile instead of the final LSE."""
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    rq, rk = (Sq + 127) // 128 * 128, (Sk + 127) // 128 * 128
+    out = np.zeros((B, H, rq, rk), dtype=np.float32)
+    if Sq == 0 or Sk == 0:
+        return out
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else softmax_scale
+    s, _, mask = _scores(q, k, scale, 0.0, alibi_slopes, causal, window_left, window_right)
+    m = np.max(s, axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0)
+    with np.errstate(divide="ignore"):  # rows without a visible key: lse = -inf, every entry masked
+        lse = m + np.log(np.sum(np.exp(s - m), axis=-1, keepdims=True))
+    p = np.where(mask, 0.0, np.exp(s - np.where(np.isfinite(lse), lse, 0.0))).astype(np.float32)
+    dropped = ~np.asarray(keep_mask, dtype=bool) & ~mask
+    out[:, :, :Sq, :Sk] = np.where(dropped, -p, p)
+    out[:, :, :Sq, :Sk][dropped & (p == 0)] = -0.0
+    return out
+
+
 def _slices(cu):
     cu = np.asarray(cu).tolist()
     return [(cu[i], cu[i + 1]) for i in range(len(cu) - 1)]

@@ -159,3 +159,25 @@ def test_varlen_equals_per_sequence_dense():
     assert delta.shape == (4, 25 + 128 * 3)  # test_gold.py:531
     np.testing.assert_allclose(delta[:, 17 + 256: 25 + 256], np.sum(dout[17:] * out[17:], -1).T, rtol=1e-5)
     assert np.all(delta[:, 17:17 + 256] == 0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_probabilities_are_the_attention_matrix(causal):
+    """|P| times V is torch's SDPA output (so |P| is the softmax attention matrix),
+    rows of visible keys sum to 1, the padding to 128 is +0, and the sign bit is
+    set exactly on the visible elements the keep mask drops."""
+    from oracle import dropout as DR
+
+    b, s, hq, hk, d = 2, 75, 4, 2, 64
+    q, k, v = rnd(b, s, hq, d, seed=11), rnd(b, s, hk, d, seed=12), rnd(b, s, hk, d, seed=13)
+    keep = DR.dense_mask(5, 64, b, hq, s, s, 0.3)
+    p = OA.probabilities(q, k, keep, causal=causal)
+    assert p.shape == (b, hq, 128, 128)
+    assert not p[:, :, s:].any() and not p[:, :, :, s:].any() and not np.signbit(p[:, :, s:]).any()
+    a = np.abs(p[:, :, :s, :s]).astype(np.float64)
+    vt = np.repeat(np.transpose(v, (0, 2, 1, 3)), hq // hk, axis=1)
+    o, _ = sdpa(q, k, v, causal)
+    np.testing.assert_allclose(np.transpose(a @ vt, (0, 2, 1, 3)), o, atol=2e-5)
+    np.testing.assert_allclose(a.sum(-1), 1.0, atol=1e-5)
+    visible = ~np.triu(np.ones((s, s), dtype=bool), 1) if causal else np.ones((s, s), dtype=bool)
+    np.testing.assert_array_equal(np.signbit(p[:, :, :s, :s]), ~keep & visible)

@@ -33,8 +33,25 @@ def test_fwd_arity_is_the_reference_table(runtime):
     assert rc == -1
     kind, msg = _err(runtime)
     assert kind == "ValueError" and "fwd expects 9 positional arguments" in msg
-    rc, _ = T.call("fwd", *([x] * 3), None, None, False, -1, -1, 0.0, 0.0, 1, 2, 3, 4)
+    # Arity 16 (native RNG reservation) and 18 (RNG descriptor) are not built.
+    rc, _ = T.call("fwd", *([x] * 3), None, None, False, -1, -1, 0.0, 0.0, 1, 2, None, True, 5, 6)
     assert rc == -1 and "not part of this build" in _err(runtime)[1]
+
+
+def test_fwd_return_softmax_validation(runtime):
+    """Arity 14 (..., p, state, offset, out, return_softmax): probabilities need
+    dropout and an RNG-state tensor, and fwd_lse cannot return them
+    (host/forward/mod.rs:181-199)."""
+    x = torch.zeros(1, 4, 1, 8, dtype=torch.half)
+    state = torch.zeros(2, dtype=torch.int64)
+    rc, _ = T.call("fwd", *([x] * 3), None, None, False, -1, -1, 0.0, 0.0, state, 0, None, True)
+    assert rc == -1
+    kind, msg = _err(runtime)
+    assert kind == "ValueError" and "return_softmax requires nonzero dropout" in msg
+    rc, _ = T.call("fwd", *([x] * 3), None, None, False, -1, -1, 0.0, 0.2, 7, 0, None, True)
+    assert rc == -1 and "RNG-state tensor" in _err(runtime)[1]
+    rc, _ = T.call("fwd_lse", *([x] * 3), None, None, False, -1, -1, 0.0, 0.2, state, 0, x, True)
+    assert rc == -1 and "cannot return diagnostic probabilities" in _err(runtime)[1]
 
 
 def test_fwd_lse_requires_an_output(runtime):

@@ -129,6 +129,18 @@ def test_forward_and_backward(runtime):
     torch.cuda.synchronize()
     assert torch.equal(o3, o3r)
 
+    # return_softmax: arity 14 (..., p, state, offset, out | None, True) -> [out, lse, probabilities]
+    state = torch.tensor([99, 4], dtype=torch.int64, device="cuda")
+    rc, res4 = T.call("fwd", *base, 0.2, state, 0, None, True)
+    _ok(rc, runtime)
+    items4 = T.array_items(res4)
+    assert len(items4) == 3
+    o4, l4, p4 = (T.tensor_of(x) for x in items4)
+    o4r, l4r, p4r = ops.fwd(*base, 0.2, state, 0, None, True)
+    torch.cuda.synchronize()
+    assert p4.shape == (2, 8, 256, 256)
+    assert torch.equal(o4, o4r) and torch.equal(l4, l4r) and torch.equal(p4, p4r)
+
     # bwd_preprocess -> delta; bwd_all -> [dq, dk, dv]; bwd_dkv; bwd_dq
     rc, rd = T.call("bwd_preprocess", do, out_r, 0.0)
     _ok(rc, runtime)
@@ -152,7 +164,7 @@ def test_forward_and_backward(runtime):
     assert torch.equal(T.tensor_of(rq.p), grads_r[0])
 
     # Every returned object goes away with one reference drop.
-    _release(runtime, res.p, res2.p, res3.p, rd.p, rb.p, rkv.p, rq.p)
+    _release(runtime, res.p, res2.p, res3.p, res4.p, rd.p, rb.p, rkv.p, rq.p)
     assert runtime.mock_live_objects() == live
 
 
