@@ -137,6 +137,17 @@ typedef struct kcr_dropout {
     const kcr_tensor* rng_state;  /* nullable */
 } kcr_dropout;
 
+/* Dropout RNG state from a generator descriptor. replaces the `rng_state(reference,
+ * seed, offset, intragraph, captured)` export (flash-attn2-rs/src/host/rng.rs:13-98,
+ * kernel src/device/rng.rs:1-26) and the descriptor step of `fwd` at arities 16
+ * and 18 (src/host/forward/mod.rs:132-178, 492-523). Writes [seed, offset] into
+ * `state` (contiguous int64 [2] on the device) on `stream`: with captured == 0
+ * the values themselves, with captured != 0 the 8-byte values at device
+ * addresses `seed` and `offset`, the offset plus `intragraph` (a reservation
+ * made under graph capture, resolved at each replay). */
+int kcr_flash_rng_state(const kcr_tensor* state, uint64_t seed, uint64_t offset, uint64_t intragraph,
+                        int captured, void* stream);
+
 /* Dense forward. replaces `fwd_lse(q,k,v,alibi,scale,causal,wl,wr,softcap,out)`
  * (flash-attn2-rs/src/host/forward/mod.rs:835-853; arities mod.rs:53-61) and `fwd`
  * (mod.rs:815-833); dropout as in mod.rs:73-199 (return_softmax: kcr_flash_fwd_softmax).

@@ -52,11 +52,17 @@ KCR_TVM_FFI_EXPORT(rms_norm_forward)
 KCR_TVM_FFI_EXPORT(rms_norm_backward)
 KCR_TVM_FFI_EXPORT(rms_norm_reduce_weight_grad)
 
-/* flash-attn2-rs/src/host/forward/mod.rs:52-61, 815-853: fwd(q, k, v,
+/* flash-attn2-rs/src/host/forward/mod.rs:52-199, 815-853: fwd(q, k, v,
  * alibi|None, scale|None, causal, wl, wr, softcap[, p, seed|state, offset]
- * [, out]) -> [out, lse]; fwd_lse(..., out) -> lse. */
+ * [, out]) -> [out, lse]; fwd_lse(..., out) -> lse. Arity 14 (..., p, state,
+ * offset, out|None, return_softmax) returns [out, lse, probabilities]; arity 16
+ * adds (reserve Function, generator) and arity 18 (seed, offset, intragraph,
+ * captured): the generator descriptor is resolved into `state` first. */
 KCR_TVM_FFI_EXPORT(fwd)
 KCR_TVM_FFI_EXPORT(fwd_lse)
+/* host/rng.rs:50-98: rng_state(reference, seed, offset, intragraph, captured)
+ * -> int64 [2] Tensor on reference's device. */
+KCR_TVM_FFI_EXPORT(rng_state)
 /* host/backward.rs:14-757: bwd_preprocess(dout, out, p) -> delta;
  * bwd_dq / bwd_dkv / bwd_all(q, k, v, dout, lse, delta, alibi, scale, causal,
  * left, right, softcap, p, rng_state) -> dq | [dk, dv] | [dq, dk, dv]. */

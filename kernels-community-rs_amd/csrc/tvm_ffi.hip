@@ -89,7 +89,7 @@ namespace ffi {
 namespace {
 
 constexpr int32_t kNone = 0, kInt = 1, kBool = 2, kFloat = 3, kDLTensorPtr = 7, kRawStr = 8, kByteArrayPtr = 9,
-                  kSmallStr = 11, kStr = 65, kTensor = 70;
+                  kSmallStr = 11, kStr = 65, kFunction = 68, kShape = 69, kTensor = 70;
 constexpr int32_t kDLCPU = 1, kDLCUDA = 2, kDLROCM = 10;
 
 // Runtime entry points of the calling process's tvm-ffi runtime (or null),
@@ -456,16 +456,71 @@ namespace kcr {
 namespace ffi {
 namespace {
 
+// The generator descriptor of fwd at arity 16 (reserve(generator, device,
+// B * H * 32) returning a 4-element Shape) or 18 (four arguments), resolved
+// into the state tensor on the call's stream (host/forward/mod.rs:132-178,
+// 492-523).
+void resolve_descriptor(const Args& a, const DLTensor* q, const DLTensor* k, const Drop& drop,
+                        bool return_softmax) {
+    const bool native = a.n == 16;
+    if (native) {
+        if (!drop.on || !drop.d.rng_state) throw value_error("native reservation requires dropout and a state tensor");
+    } else {
+        if (!drop.on || q->ndim != 4 || k->ndim != 4 || !drop.d.rng_state || q->shape[3] != 64 || q->shape[1] == 0 ||
+            k->shape[1] == 0) {
+            throw value_error("RNG descriptor requires nonempty D64 dropout");
+        }
+        if (return_softmax) throw value_error("RNG descriptor does not support diagnostic probabilities");
+    }
+    uint64_t desc[3];
+    int captured;
+    if (native) {
+        if (a.at(14).type_index != kFunction) a.bad(14, "a Function (reserve)");
+        const FunctionCallFn call = runtime_fn<FunctionCallFn>("TVMFFIFunctionCall");
+        const DecRefFn dec = runtime_fn<DecRefFn>("TVMFFIObjectDecRef");
+        if (!call) throw runtime_error("native reservation needs the tvm-ffi runtime (TVMFFIFunctionCall)");
+        TVMFFIAny args[3]{};
+        args[0].type_index = kInt;
+        args[0].v_int64 = a.i64(15);
+        args[1].type_index = kInt;
+        args[1].v_int64 = q->device.device_id;
+        args[2].type_index = kInt;
+        args[2].v_int64 = q->shape[0] * q->shape[2] * 32;
+        TVMFFIAny out{};
+        if (call(a.at(14).v_ptr, args, 3, &out) != 0) throw runtime_error("reserve failed");
+        if (out.type_index != kShape) {
+            if (out.type_index >= kStr && dec) dec(out.v_ptr);
+            throw type_error("reserve must return a Shape descriptor");
+        }
+        // ShapeObj: the object header, then {const int64_t* data; int64_t size}.
+        const char* body = static_cast<const char*>(out.v_ptr) + sizeof(ObjectHeader);
+        const int64_t* values = *reinterpret_cast<const int64_t* const*>(body);
+        const int64_t size = *reinterpret_cast<const int64_t*>(body + sizeof(void*));
+        const bool ok = size == 4 && (values[3] == 0 || values[3] == 1);
+        if (ok) {
+            for (int i = 0; i < 3; ++i) desc[i] = static_cast<uint64_t>(values[i]);
+            captured = static_cast<int>(values[3]);
+        }
+        if (dec) dec(out.v_ptr);
+        if (!ok) throw value_error("invalid reserved RNG descriptor");
+    } else {
+        for (int i = 0; i < 3; ++i) desc[i] = static_cast<uint64_t>(a.i64(14 + i));
+        captured = a.boolean(17) ? 1 : 0;
+    }
+    if (captured && (desc[0] == 0 || desc[1] == 0 || desc[0] % 8 != 0 || desc[1] % 8 != 0)) {
+        throw value_error(native ? "invalid reserved capture pointers" : "invalid capture descriptor pointers");
+    }
+    check_status(kcr_flash_rng_state(drop.d.rng_state, desc[0], desc[1], desc[2], captured, stream_for(q)));
+}
+
 // fwd / fwd_lse (host/forward/mod.rs:52-61, 815-853): 9 base arguments, then
 // optionally (p, seed | state, offset) and/or the output tensor; arity 14 is
 // (..., p, state, offset, out | None, return_softmax) and returns
-// [out, lse, probabilities] (mod.rs:133-199, 382-398).
+// [out, lse, probabilities] (mod.rs:133-199, 382-398); arities 16 and 18 add a
+// generator descriptor.
 void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
     const int n = a.n;
-    if (n == 16 || n == 18) {
-        throw runtime_error("generator-descriptor RNG reservation (fwd arities 16/18) is not part of this build");
-    }
-    if (n != 9 && n != 10 && n != 12 && n != 13 && n != 14) {
+    if (n != 9 && n != 10 && n != 12 && n != 13 && n != 14 && n != 16 && n != 18) {
         throw value_error("fwd expects 9 positional arguments (q, k, v, alibi_slopes, softmax_scale, is_causal, "
                           "window_size_left, window_size_right, softcap), optionally followed by p_dropout, "
                           "seed, offset, and/or an output tensor; got " +
@@ -473,12 +528,17 @@ void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
     }
     const DLTensor* q = a.dltensor(0);
     if (q->ndim != 4) throw value_error("q must have 4 dimensions [B, S, H, D]");
-    const int out_idx = n == 14 ? 12 : n - 1;
-    const bool supplied = n == 10 || n == 13 || (n == 14 && !a.none(12));
-    const bool return_softmax = n == 14 && a.boolean(13);
+    const bool wide = n == 14 || n == 16 || n == 18;
+    const int out_idx = wide ? 12 : n - 1;
+    const bool supplied = n == 10 || n == 13 || (wide && !a.none(12));
+    const bool return_softmax = wide && a.boolean(13);
     if (lse_only && !supplied) throw value_error("LSE-only forward requires a supplied output");
     if (lse_only && return_softmax) throw value_error("LSE-only forward cannot return diagnostic probabilities");
     const Drop drop = n >= 12 ? dropout_of(a, 9, 10, 11, false) : Drop{};
+    if (drop.d.rng_state && drop.d.offset != 0) {
+        throw value_error("offset must be zero when seed is an RNG-state tensor");
+    }
+    if (n == 16 || n == 18) resolve_descriptor(a, q, a.dltensor(1), drop, return_softmax);
     if (return_softmax && (!drop.on || !drop.d.rng_state)) {
         throw value_error("return_softmax requires nonzero dropout and a CUDA RNG-state tensor");
     }
@@ -508,7 +568,7 @@ void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
         check_status(kcr_flash_fwd(vq.ptr(), vk.ptr(), vv.ptr(), al.ptr(), has_scale, scale,
                                    a.boolean(5) ? 1 : 0, a.i64(6), a.i64(7), a.f64(8), drop.ptr(), vo.ptr(),
                                    vl.ptr(), stream_for(q)));
-        if (n == 14) probs = alloc({0}, q->dtype, q->device);
+        if (wide) probs = alloc({0}, q->dtype, q->device);
     }
     if (lse_only) {
         set_tensor(r, lse);
@@ -531,7 +591,7 @@ void fwd_impl(const Args& a, TVMFFIAny* r, bool lse_only) {
         items.push_back(std::move(out_o));
     }
     items.push_back(std::move(lse));
-    if (n == 14) items.push_back(std::move(probs));
+    if (wide) items.push_back(std::move(probs));
     set_array(r, items);
 }
 
@@ -593,6 +653,27 @@ void bwd_impl(const Args& a, TVMFFIAny* r, bool want_q, bool want_kv) {
 extern "C" int32_t __tvm_ffi_fwd(void*, const TVMFFIAny* args, int32_t n, TVMFFIAny* result) {
     return kcr::ffi::packed("fwd", args, n, result,
                             [&](const Args& a, TVMFFIAny* r) { kcr::ffi::fwd_impl(a, r, false); });
+}
+
+extern "C" int32_t __tvm_ffi_rng_state(void*, const TVMFFIAny* args, int32_t n, TVMFFIAny* result) {
+    return kcr::ffi::packed("rng_state", args, n, result, [&](const Args& a, TVMFFIAny* r) {
+        if (a.n != 5) throw kcr::value_error("rng_state expects reference, seed, offset, intragraph, captured");
+        const auto* ref = a.dltensor(0);
+        if (ref->device.device_type != kcr::ffi::kDLCUDA && ref->device.device_type != kcr::ffi::kDLROCM) {
+            throw kcr::value_error("RNG state requires a CUDA reference tensor");
+        }
+        const uint64_t seed = static_cast<uint64_t>(a.i64(1)), offset = static_cast<uint64_t>(a.i64(2));
+        const uint64_t intragraph = static_cast<uint64_t>(a.i64(3));
+        const int captured = a.boolean(4) ? 1 : 0;
+        if (captured && (seed == 0 || offset == 0 || seed % 8 != 0 || offset % 8 != 0)) {
+            throw kcr::value_error("captured RNG descriptor requires aligned non-null CUDA pointers");
+        }
+        Owned state = kcr::ffi::alloc({2}, kcr::ffi::DLDataType{0, 64, 1}, ref->device);
+        const View vs = kcr::ffi::view_of(state.dl, a.op);
+        kcr::ffi::check_status(kcr_flash_rng_state(vs.ptr(), seed, offset, intragraph, captured,
+                                                   kcr::ffi::stream_for(ref)));
+        kcr::ffi::set_tensor(r, state);
+    });
 }
 
 extern "C" int32_t __tvm_ffi_fwd_lse(void*, const TVMFFIAny* args, int32_t n, TVMFFIAny* result) {

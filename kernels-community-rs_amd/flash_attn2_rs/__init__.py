@@ -17,6 +17,7 @@ from .flash_attn_interface import (
     fwd,
     fwd_explicit,
     fwd_kvcache,
+    reserve_rng_state,
     varlen_bwd,
     varlen_fwd,
 )
@@ -30,6 +31,7 @@ __all__ = [
     "varlen_bwd",
     "fwd_explicit",
     "fwd_kvcache",
+    "reserve_rng_state",
     "flash_attn_func",
     "flash_attn_qkvpacked_func",
     "flash_attn_kvpacked_func",

@@ -5,6 +5,12 @@ positional signatures and return conventions, backed by libkcr_hip.so.
       -> [out, lse]                          host/forward/mod.rs:52-61, 815-833
   fwd(..., p, state, offset, out, return_softmax)
       -> [out, lse, probabilities]           host/forward/mod.rs:133-199, 382-398
+  fwd(..., p, state, 0, out, return_softmax, reserve, generator)      (arity 16)
+  fwd(..., p, state, 0, out, return_softmax, seed, offset, intragraph, captured)
+      (arity 18): the generator descriptor is resolved into `state` first
+                                             host/forward/mod.rs:132-178, 492-523
+  rng_state(reference, seed, offset, intragraph, captured) -> int64 [2]
+                                             host/rng.rs:50-98
   fwd_lse(..., out) -> lse                   host/forward/mod.rs:835-853
   varlen_fwd_explicit(q, k, v, cuq, cuk, seqused_k, leftpad_k, alibi, scale, causal,
       left, right, softcap, p, state, max_q, max_k, return_softmax, zero_tensors)
@@ -29,8 +35,8 @@ whose rows are not 16-byte aligned are repacked first, as the reference does
 with `copy_attention_layout` (host/layout.rs:46-125). Dropout follows the
 reference's Philox4x32-7 mask stream, keyed by explicit (seed, offset) or by a
 device int64 [2] RNG-state tensor. Diagnostic probabilities (return_softmax)
-come from kcr_flash_fwd_softmax / kcr_flash_varlen_fwd_softmax; the
-generator-descriptor arities (16 and 18) are not part of this build.
+come from kcr_flash_fwd_softmax / kcr_flash_varlen_fwd_softmax; generator
+descriptors (arities 16 and 18, `rng_state`) from kcr_flash_rng_state.
 """
 
 from __future__ import annotations
@@ -85,12 +91,61 @@ def _scale_args(scale):
     return (0, ctypes.c_double(0.0)) if scale is None else (1, ctypes.c_double(float(scale)))
 
 
+def _u64(x):
+    return ctypes.c_uint64(int(x) & 0xFFFF_FFFF_FFFF_FFFF)
+
+
+def _resolve_descriptor(state, descriptor, captured):
+    """Writes the [seed, offset] of a generator descriptor into `state` on the
+    current stream (host/rng.rs:13-47)."""
+    seed, offset, intragraph = descriptor
+    call("kcr_flash_rng_state", ref(describe(state)), _u64(seed), _u64(offset), _u64(intragraph),
+         int(bool(captured)), stream_of(state))
+
+
+def rng_state(reference, seed, offset, intragraph, captured):
+    """CUDA int64 [seed, offset] from a Philox descriptor (host/rng.rs:50-78)."""
+    if not isinstance(reference, torch.Tensor) or not reference.is_cuda:
+        raise ValueError("RNG state requires a CUDA reference tensor")
+    state = torch.empty(2, dtype=torch.int64, device=reference.device)
+    _resolve_descriptor(state, (seed, offset, intragraph), captured)
+    return state
+
+
+def _fwd_descriptor(args, n, q, k, p, state, return_softmax):
+    """Arities 16 (reserve callback, generator) and 18 (seed, offset, intragraph,
+    captured): the descriptor is resolved into the state tensor, which the
+    forward then reads (host/forward/mod.rs:132-178, 492-523)."""
+    dropout = float(np.float32(p)) > 0.0
+    if n == 16:
+        if not dropout or state is None:
+            raise ValueError("native reservation requires dropout and a state tensor")
+    else:
+        if (not dropout or q.ndim != 4 or k.ndim != 4 or state is None or q.shape[3] != 64
+                or q.shape[1] == 0 or k.shape[1] == 0):
+            raise ValueError("RNG descriptor requires nonempty D64 dropout")
+        if return_softmax:
+            raise ValueError("RNG descriptor does not support diagnostic probabilities")
+    if not _rng_state_ok(state, q):
+        raise ValueError("rng_state must be a contiguous CUDA int64 tensor of shape [2] on q's device")
+    if n == 16:
+        reserve, generator = args[14], int(args[15])
+        values = [int(x) for x in reserve(generator, q.device.index or 0, q.shape[0] * q.shape[2] * 32)]
+        if len(values) != 4 or values[3] not in (0, 1):
+            raise ValueError("invalid reserved RNG descriptor")
+        descriptor, captured = values[:3], values[3]
+        what = "invalid reserved capture pointers"
+    else:
+        descriptor, captured = [int(x) for x in args[14:17]], int(bool(args[17]))
+        what = "invalid capture descriptor pointers"
+    if captured and (descriptor[0] == 0 or descriptor[1] == 0 or descriptor[0] % 8 or descriptor[1] % 8):
+        raise ValueError(what)
+    _resolve_descriptor(state, descriptor, captured)
+
+
 def _fwd_impl(args, lse_only):
     n = len(args)
-    if n in (16, 18):
-        raise NotImplementedError(
-            "generator-descriptor RNG reservation (fwd arities 16/18) is not part of this build")
-    if n not in (9, 10, 12, 13, 14):
+    if n not in (9, 10, 12, 13, 14, 16, 18):
         raise ValueError(
             "fwd expects 9 positional arguments (q, k, v, alibi_slopes, softmax_scale, "
             "is_causal, window_size_left, window_size_right, softcap), optionally followed by "
@@ -105,8 +160,10 @@ def _fwd_impl(args, lse_only):
         else:
             seed = int(args[10])
         offset = int(args[11])
-    return_softmax = n == 14 and bool(args[13])
-    supplied = args[12] if n == 14 else args[-1] if n in (10, 13) else None
+    if offset != 0 and state is not None:
+        raise ValueError("offset must be zero when seed is an RNG-state tensor")
+    return_softmax = n in (14, 16, 18) and bool(args[13])
+    supplied = args[12] if n in (14, 16, 18) else args[-1] if n in (10, 13) else None
     if lse_only and supplied is None:
         raise ValueError("LSE-only forward requires a supplied output")
     if lse_only and return_softmax:
@@ -115,6 +172,8 @@ def _fwd_impl(args, lse_only):
         raise ValueError("return_softmax requires nonzero dropout and a CUDA RNG-state tensor")
     if q.ndim != 4:
         raise ValueError(f"q must have 4 dimensions [B, S, H, D], got shape {list(q.shape)}")
+    if n in (16, 18):
+        _fwd_descriptor(args, n, q, k, p, state, return_softmax)
     b, sq, h, d = q.shape
     # Misaligned or strided inputs and an output that the kernels cannot write
     # in place are staged through packed copies inside the C ABI
@@ -136,7 +195,7 @@ def _fwd_impl(args, lse_only):
          stream_of(q))
     if lse_only:
         return lse
-    if n == 14:
+    if n in (14, 16, 18):
         return [out, lse, torch.empty(0, dtype=q.dtype, device=q.device)]
     return [out, lse]
 
@@ -506,6 +565,7 @@ def fwd_kvcache(q, kcache, vcache, k=None, v=None, seqlens_k=None, rotary_cos=No
 
 
 ops = SimpleNamespace(
+    rng_state=rng_state,
     fwd=fwd,
     fwd_lse=fwd_lse,
     varlen_fwd_explicit=varlen_fwd_explicit,

@@ -12,10 +12,11 @@ that matters on this path (dtype, device, shapes, head size, GQA divisibility).
 Dropout uses the reference's Philox4x32-7 mask stream keyed by a CUDA int64 [2]
 RNG-state tensor [seed, offset], returned by the forward and passed to the
 backward. The reference reserves those values with
-`torch.Generator.philox_state` (Torch >= 2.14); this build draws them from the
-generator with `torch.randint`, so the stream is reproducible under
-`torch.manual_seed`, and a caller that passes the same [seed, offset] gets the
-reference's masks. With return_softmax the forward also returns the diagnostic
+`torch.Generator.philox_state` (Torch >= 2.14). On older Torch this build
+reserves them from the generator's seed and Philox offset, advancing the offset
+by the same increment, so a generator in the same state gives the reference's
+[seed, offset] and masks (under graph capture on older Torch, fresh values
+drawn with `torch.randint`). With return_softmax the forward also returns the diagnostic
 probabilities [B, H, ceil128(Sq), ceil128(Sk)]: the softmax probability of each
 visible element, its sign bit set where dropout drops it.
 """
@@ -42,13 +43,64 @@ def _check_dropout(p, softcap=0.0):
     return p
 
 
-def _new_rng_state(q, gen=None):
-    """CUDA int64 [seed, offset] drawn from `gen` (default: the device's CUDA
-    generator), without a host synchronisation."""
+def _descriptor_values(generator, increment):
+    """A Philox reservation of `increment` from a CUDA generator as (seed, offset,
+    intragraph, captured). With torch.Generator.philox_state (Torch >= 2.14) this
+    is that reservation, made atomically by Torch, as the reference makes it
+    (flash_attn_interface.py:53-73). Without it, outside graph capture, the same
+    values come from the generator's seed and Philox offset, which then advances
+    by the increment rounded to a multiple of 4, as Torch's own reservation does.
+    Under graph capture on older Torch no capture-safe reservation exists, and
+    fresh values are drawn from the generator with torch.randint instead."""
+    reserve = getattr(generator, "philox_state", None)
+    if reserve is not None:
+        seed, offset, intragraph = reserve(increment)
+        captured = seed.is_cuda
+        return (seed.data_ptr() if captured else seed.item(), offset.data_ptr() if captured else offset.item(),
+                intragraph.item(), int(captured))
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    seed, offset = generator.initial_seed(), generator.get_offset()
+    generator.set_offset(offset + (increment + 3) // 4 * 4)
+    return seed, offset, 0, 0
+
+
+def _reserve_rng_state(q, batch, heads, gen=None):
+    """CUDA int64 [seed, offset] reserving FlashAttention-2's batch*heads*32 Philox
+    increment from `gen` (default: the device's CUDA generator), without a host
+    synchronisation (flash_attn_interface.py:36-44)."""
     if gen is not None and not isinstance(gen, torch.Generator):
         raise RuntimeError("gen must be a torch.Generator")
     g = gen if gen is not None else torch.cuda.default_generators[q.device.index or 0]
-    return torch.randint(-(2**63), 2**63 - 1, (2,), device=q.device, dtype=torch.int64, generator=g)
+    if g.device.type != "cuda":
+        raise RuntimeError("gen must be a CUDA torch.Generator")
+    with torch.cuda.device(q.device):
+        values = _descriptor_values(g, int(batch) * int(heads) * 32)
+        if values is None:
+            return torch.randint(-(2**63), 2**63 - 1, (2,), device=q.device, dtype=torch.int64, generator=g)
+        seed, offset, intragraph, captured = values
+        return ops.rng_state(q, seed, offset, intragraph, bool(captured))
+
+
+def reserve_rng_state(q, gen=None):
+    """Reserve FlashAttention-2's B*H*32 Philox increment and return CUDA int64
+    [seed, offset] (flash_attn_interface.py:20-33)."""
+    if not isinstance(q, torch.Tensor) or not q.is_cuda or q.ndim != 4:
+        raise ValueError("q must be a CUDA tensor of shape [B, S, H, D]")
+    if q.shape[0] <= 0 or q.shape[2] <= 0:
+        raise ValueError("q must have positive batch and head counts")
+    if gen is not None:
+        if not isinstance(gen, torch.Generator) or gen.device.type != "cuda":
+            raise TypeError("gen must be a CUDA torch.Generator")
+        if gen.device.index not in (None, q.device.index):
+            raise ValueError("gen must be on q's device")
+    return _reserve_rng_state(q, q.shape[0], q.shape[2], gen)
+
+
+def _new_rng_state(q, gen=None, batch=None, heads=None):
+    if batch is None:
+        batch, heads = q.shape[0], q.shape[2]
+    return _reserve_rng_state(q, batch, heads, gen)
 
 
 def _check_return_softmax(return_softmax, p):
@@ -217,7 +269,8 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, le
         softmax_scale = 1.0 / (q.shape[-1] ** 0.5)
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.contiguous()
-    state = _new_rng_state(q, gen) if p > 0 else torch.empty(2, device=q.device, dtype=torch.int64)
+    state = (_new_rng_state(q, gen, cu_seqlens_q.numel() - 1, q.shape[1]) if p > 0
+             else torch.empty(2, device=q.device, dtype=torch.int64))
     output, lse, probabilities = ops.varlen_fwd_explicit(
         q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi_slopes,
         float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),
@@ -254,7 +307,7 @@ def varlen_bwd(dout, q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, dq=N
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.contiguous()
     if p > 0 and rng_state is None:
-        rng_state = _new_rng_state(q, gen)
+        rng_state = _new_rng_state(q, gen, batch, h)
     grad_q, grad_k, grad_v, softmax_d = ops.varlen_bwd_explicit(
         q, k, v, dout, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, alibi_slopes,
         float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),

@@ -33,9 +33,8 @@ def test_fwd_arity_is_the_reference_table(runtime):
     assert rc == -1
     kind, msg = _err(runtime)
     assert kind == "ValueError" and "fwd expects 9 positional arguments" in msg
-    # Arity 16 (native RNG reservation) and 18 (RNG descriptor) are not built.
-    rc, _ = T.call("fwd", *([x] * 3), None, None, False, -1, -1, 0.0, 0.0, 1, 2, None, True, 5, 6)
-    assert rc == -1 and "not part of this build" in _err(runtime)[1]
+    rc, _ = T.call("fwd", *([x] * 3), None, None, False, -1, -1, 0.0, 0.0, 1, 2, None, True, 5)
+    assert rc == -1 and "fwd expects 9 positional arguments" in _err(runtime)[1]
 
 
 def test_fwd_return_softmax_validation(runtime):
@@ -86,3 +85,38 @@ def test_backward_needs_fourteen_arguments(runtime):
     x = torch.zeros(1, 4, 1, 8, dtype=torch.half)
     rc, _ = T.call("bwd_all", x, x, x)
     assert rc == -1 and "backward component expects" in _err(runtime)[1]
+
+
+def test_fwd_descriptor_arities_validation(runtime):
+    """Arity 16 calls reserve(generator, device, B*H*32) and needs a 4-element
+    Shape; arity 18 needs nonempty D64 dropout and aligned capture pointers
+    (host/forward/mod.rs:132-178, 492-523). All fail before any device work."""
+    x = torch.zeros(2, 4, 3, 64, dtype=torch.half)
+    state = torch.zeros(2, dtype=torch.int64)
+    base = (x, x, x, None, None, False, -1, -1, 0.0)
+    reserve = T.make_reserve(1, 2, 3)  # three values: invalid
+    rc, _ = T.call("fwd", *base, 0.0, state, 0, None, False, reserve, 7)
+    assert rc == -1 and "native reservation requires dropout" in _err(runtime)[1]
+    rc, _ = T.call("fwd", *base, 0.2, state, 0, None, False, reserve, 7)
+    assert rc == -1 and "invalid reserved RNG descriptor" in _err(runtime)[1]
+    assert runtime.mock_reserve_calls(reserve.ptr) == 1
+    assert [runtime.mock_reserve_arg(reserve.ptr, i) for i in range(3)] == [7, 0, 2 * 3 * 32]
+    rc, _ = T.call("fwd", *base, 0.2, state, 0, None, False, T.make_reserve(8, 0, 0, 1), 7)
+    assert rc == -1 and "invalid reserved capture pointers" in _err(runtime)[1]
+    rc, _ = T.call("fwd", *base, 0.2, state, 0, None, False, 1, 2, 0, True)
+    assert rc == -1 and "invalid capture descriptor pointers" in _err(runtime)[1]
+    rc, _ = T.call("fwd", *base, 0.2, state, 0, None, True, 1, 2, 0, False)
+    assert rc == -1 and "does not support diagnostic probabilities" in _err(runtime)[1]
+    y = torch.zeros(1, 4, 1, 128, dtype=torch.half)
+    rc, _ = T.call("fwd", y, y, y, None, None, False, -1, -1, 0.0, 0.2, state, 0, None, False, 1, 2, 0, False)
+    assert rc == -1 and "RNG descriptor requires nonempty D64 dropout" in _err(runtime)[1]
+    rc, _ = T.call("fwd", *base, 0.2, state, 3, None, False, 1, 2, 0, False)
+    assert rc == -1 and "offset must be zero" in _err(runtime)[1]
+
+
+def test_rng_state_export_validation(runtime):
+    x = torch.zeros(4)
+    rc, _ = T.call("rng_state", x, 1, 2, 3)
+    assert rc == -1 and "rng_state expects reference" in _err(runtime)[1]
+    rc, _ = T.call("rng_state", x, 1, 2, 3, False)
+    assert rc == -1 and "CUDA reference tensor" in _err(runtime)[1]

@@ -201,3 +201,41 @@ def test_varlen(runtime):
         assert torch.equal(a, b)
     _release(runtime, rf.p, rb.p)
     assert runtime.mock_live_objects() == live
+
+
+def test_rng_descriptors(runtime):
+    """rng_state and fwd at arities 16 (reserve Function returning a Shape) and
+    18 (explicit descriptor) equal the explicit-seed forward bit for bit."""
+    import flash_attn2_rs
+
+    ops = flash_attn2_rs.ops
+    q, k, v, _ = _attn(d=64)
+    live = runtime.mock_live_objects()
+    base = (q, k, v, None, None, True, -1, -1, 0.0)
+    seed, offset = 4242, 96
+    ref_out, ref_lse = ops.fwd(*base, 0.2, seed, offset)
+
+    rc, rs = T.call("rng_state", q, seed, offset, 0, False)
+    _ok(rc, runtime)
+    torch.cuda.synchronize()
+    assert T.tensor_of(rs.p).tolist() == [seed, offset]
+
+    state = torch.empty(2, dtype=torch.int64, device="cuda")
+    rc, r18 = T.call("fwd", *base, 0.2, state, 0, None, False, seed, offset, 0, False)
+    _ok(rc, runtime)
+    o18, l18, p18 = (T.tensor_of(x) for x in T.array_items(r18))
+    torch.cuda.synchronize()
+    assert torch.equal(o18, ref_out) and torch.equal(l18, ref_lse) and p18.numel() == 0
+    assert state.tolist() == [seed, offset]
+
+    reserve = T.make_reserve(seed, offset, 0, 0)
+    state2 = torch.empty(2, dtype=torch.int64, device="cuda")
+    rc, r16 = T.call("fwd", *base, 0.2, state2, 0, None, False, reserve, 3)
+    _ok(rc, runtime)
+    o16 = T.tensor_of(T.array_items(r16)[0])
+    torch.cuda.synchronize()
+    assert torch.equal(o16, ref_out) and state2.tolist() == [seed, offset]
+    assert [runtime.mock_reserve_arg(reserve.ptr, i) for i in range(3)] == [3, q.device.index, 2 * 8 * 32]
+
+    _release(runtime, rs.p, r18.p, r16.p)
+    assert runtime.mock_live_objects() == live

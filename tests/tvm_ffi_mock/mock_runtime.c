@@ -20,6 +20,9 @@ typedef struct { int32_t type_index; uint32_t small; union { int64_t i; double f
 typedef struct { Header h; DLTensor dl; int64_t shape[8]; } Tensor;
 typedef struct { Header h; int64_t size; void* items[16]; } Array;
 typedef struct { Header h; } Function;
+typedef struct { Header h; const int64_t* data; int64_t size; int64_t values[8]; } Shape;
+/* A reserve function: returns a Shape of its stored values, records its call. */
+typedef struct { Header h; int64_t size; int64_t values[8]; int64_t last_args[3]; int64_t calls; } Reserve;
 
 static void* (*g_alloc)(int64_t bytes, int32_t device_id);
 static void* g_stream;
@@ -36,6 +39,17 @@ int64_t mock_array_size(void* a) { return ((Array*)a)->size; }
 void* mock_array_item(void* a, int64_t i) { return ((Array*)a)->items[i]; }
 DLTensor* mock_tensor(void* t) { return &((Tensor*)t)->dl; }
 uint64_t mock_refs(void* o) { return ((Header*)o)->refs; }
+
+void* mock_make_reserve(const int64_t* values, int64_t size) {
+    Reserve* r = (Reserve*)calloc(1, sizeof(Reserve));
+    r->h.refs = 1;
+    r->h.type_index = 68;
+    r->size = size > 8 ? 8 : size;
+    memcpy(r->values, values, sizeof(int64_t) * r->size);
+    return r;
+}
+int64_t mock_reserve_calls(void* r) { return ((Reserve*)r)->calls; }
+int64_t mock_reserve_arg(void* r, int i) { return ((Reserve*)r)->last_args[i]; }
 
 void* TVMFFIEnvGetStream(int32_t device_type, int32_t device_id) {
     (void)device_type; (void)device_id;
@@ -59,7 +73,7 @@ int TVMFFIObjectDecRef(void* obj) {
             Array* a = (Array*)obj;
             for (int64_t i = 0; i < a->size; ++i) TVMFFIObjectDecRef(a->items[i]);
         }
-        if (h->type_index == 70 || h->type_index == 71) {
+        if (h->type_index == 70 || h->type_index == 71 || h->type_index == 69) {
             g_live--;
             free(obj);  /* device memory stays with the test's allocator */
         }
@@ -99,7 +113,24 @@ int TVMFFIFunctionGetGlobal(const ByteArray* name, void** out) {
 }
 
 int TVMFFIFunctionCall(void* fn, Any* args, int32_t n, Any* result) {
-    if (fn != &g_array_fn || n > 16) return -1;
+    if (fn != &g_array_fn) {
+        Reserve* r = (Reserve*)fn;
+        if (n != 3) return -1;
+        for (int i = 0; i < 3; ++i) r->last_args[i] = args[i].i;
+        r->calls++;
+        Shape* sh = (Shape*)calloc(1, sizeof(Shape));
+        sh->h.refs = 1;
+        sh->h.type_index = 69;
+        memcpy(sh->values, r->values, sizeof(int64_t) * r->size);
+        sh->data = sh->values;
+        sh->size = r->size;
+        g_live++;
+        result->type_index = 69;
+        result->small = 0;
+        result->p = sh;
+        return 0;
+    }
+    if (n > 16) return -1;
     Array* a = (Array*)calloc(1, sizeof(Array));
     a->h.refs = 1;
     a->h.type_index = 71;

@@ -13,7 +13,7 @@ import torch
 
 MOCK_SRC = Path(__file__).resolve().parent / "tvm_ffi_mock" / "mock_runtime.c"
 
-NONE, INT, BOOL, FLOAT, DLTENSOR_PTR, RAW_STR, SMALL_STR, TENSOR, ARRAY = 0, 1, 2, 3, 7, 8, 11, 70, 71
+NONE, INT, BOOL, FLOAT, DLTENSOR_PTR, RAW_STR, SMALL_STR, FUNCTION, TENSOR, ARRAY = 0, 1, 2, 3, 7, 8, 11, 68, 70, 71
 DL_ROCM = 10
 
 
@@ -68,7 +68,26 @@ def mock():
         _mock.mock_refs.argtypes = [ctypes.c_void_p]
         _mock.TVMFFIObjectDecRef.argtypes = [ctypes.c_void_p]
         _mock.mock_set_stream.argtypes = [ctypes.c_void_p]
+        _mock.mock_make_reserve.restype = ctypes.c_void_p
+        _mock.mock_make_reserve.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int64]
+        _mock.mock_reserve_calls.restype = ctypes.c_int64
+        _mock.mock_reserve_calls.argtypes = [ctypes.c_void_p]
+        _mock.mock_reserve_arg.restype = ctypes.c_int64
+        _mock.mock_reserve_arg.argtypes = [ctypes.c_void_p, ctypes.c_int]
     return _mock
+
+
+class Function:
+    """A tvm-ffi Function object argument (the mock's reserve function)."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
+def make_reserve(*values):
+    """A reserve Function returning Shape(values) and recording its arguments."""
+    arr = (ctypes.c_int64 * max(len(values), 1))(*values)
+    return Function(mock().mock_make_reserve(arr, len(values)))
 
 
 _ALLOC_T = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32)
@@ -122,6 +141,8 @@ def pack(*values):
         elif isinstance(x, torch.Tensor):
             d = dltensor(x)
             a.type_index, a.p = DLTENSOR_PTR, ctypes.addressof(d)
+        elif isinstance(x, Function):
+            a.type_index, a.p = FUNCTION, x.ptr
         else:
             raise TypeError(type(x))
     return arr
