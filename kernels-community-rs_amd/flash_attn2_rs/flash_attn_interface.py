@@ -173,7 +173,7 @@ def fwd(q, k, v, out=None, alibi_slopes=None, p_dropout=0.0, softmax_scale=None,
         else:
             lse = ops.fwd_lse(*args, p, state, 0, out)
     else:
-        state = torch.empty(2, device=q.device, dtype=torch.int64)
+        state = torch.zeros(2, device=q.device, dtype=torch.int64)
         lse = ops.fwd_lse(*args, out)
     return [out, lse, probabilities, state]
 
@@ -258,7 +258,7 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, le
         if out is not None:
             out.copy_(output)
             output = out
-        return [output, lse, probabilities, torch.empty(2, device=q.device, dtype=torch.int64)]
+        return [output, lse, probabilities, torch.zeros(2, device=q.device, dtype=torch.int64)]
     p = _check_dropout(p_dropout, softcap)
     _check_return_softmax(return_softmax, p)
     _validate(q, k, v, out, alibi_slopes, softcap, packed=True)
@@ -270,7 +270,7 @@ def varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, out=None, seqused_k=None, le
     if alibi_slopes is not None:
         alibi_slopes = alibi_slopes.contiguous()
     state = (_new_rng_state(q, gen, cu_seqlens_q.numel() - 1, q.shape[1]) if p > 0
-             else torch.empty(2, device=q.device, dtype=torch.int64))
+             else torch.zeros(2, device=q.device, dtype=torch.int64))
     output, lse, probabilities = ops.varlen_fwd_explicit(
         q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, alibi_slopes,
         float(softmax_scale), bool(is_causal), int(window_size_left), int(window_size_right),

@@ -190,3 +190,31 @@ def test_varlen_grouped_decode_lse():
     scores = torch.einsum("bhd,bkhd->bhk", q.double(), k.double().repeat_interleave(4, 2)) / math.sqrt(128)
     np.testing.assert_allclose(lse.cpu().numpy(), scores.logsumexp(-1).T.numpy(), atol=5e-3, rtol=0)
     assert lse.is_contiguous() and lse.shape == (8, 16)
+
+
+def test_attention_custom_ops_opcheck():
+    """torch.library.opcheck of the custom ops behind flash_attn_func and
+    flash_attn_varlen_func (schema, fake tensors incl. the probabilities shape,
+    AOT dispatch), mirroring tvm-ffi-ext/flash_attn2_rs/_torch_interface.py:19-555."""
+    import flash_attn2_rs  # noqa: F401
+
+    ns = torch.ops.kcr_flash_attn2
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(2, 70, 4, 64, generator=g).bfloat16().cuda()
+    k = torch.randn(2, 90, 2, 64, generator=g).bfloat16().cuda()
+    v = torch.randn(2, 90, 2, 64, generator=g).bfloat16().cuda()
+    scale = 64 ** -0.5
+    torch.library.opcheck(ns._dense_forward, (q, k, v, scale, True, -1, -1, 0.0, None, 0.0, False))
+    out, lse, _, state = ns._dense_forward(q, k, v, scale, True, -1, -1, 0.0, None, 0.0, False)
+    torch.library.opcheck(ns._dense_backward,
+                          (torch.randn_like(out), q, k, v, out, lse, scale, True, -1, -1, 0.0, None, False,
+                           0.0, None))
+    cu = torch.tensor([0, 30, 70], dtype=torch.int32, device="cuda")
+    cuk = torch.tensor([0, 50, 90], dtype=torch.int32, device="cuda")
+    qv, kv, vv = q[0], k[0], v[0]
+    torch.library.opcheck(ns._varlen_forward, (qv, kv, vv, cu, cuk, 40, 50, scale, True, -1, -1, 0.0, None,
+                                               0.0, False))
+    out, lse, _, _ = ns._varlen_forward(qv, kv, vv, cu, cuk, 40, 50, scale, True, -1, -1, 0.0, None, 0.0, False)
+    torch.library.opcheck(ns._varlen_backward,
+                          (torch.randn_like(out), qv, kv, vv, out, lse, cu, cuk, 40, 50, scale, True, -1, -1,
+                           0.0, None, 0.0, None))
