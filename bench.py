@@ -93,7 +93,7 @@ def wl_rmsnorm_bwd():
 
     # Algorithmic: read x, dy, w, rstd; write dx, dw (the partials are overhead).
     bytes_ = rows * n * 2 * 3 + n * 2 * 2 + rows * 4
-    return dict(run=run, work=bytes_, bound="hbm", kernel="rms_bwd_wave",
+    return dict(run=run, work=bytes_, bound="hbm", kernel="rms_bwd_split",
                 config={"x": [rows, n], "dtype": "bf16", "casting_mode": "llama"}, cpu=None)
 
 
