@@ -277,6 +277,22 @@ def wl_hbm_copy():
                 config={"x": list(x.shape), "dtype": "bf16"}, cpu=None)
 
 
+def wl_gemm_ceiling():
+    """The MFMA rate a GEMM reaches under the board's power cap: torch.matmul
+    (hipBLASLt) of two 8192 x 8192 bf16 matrices, 2 * 8192^3 FLOP per call."""
+    g = _gen(4)
+    n = 8192
+    a = torch.randn(n, n, generator=g).bfloat16().cuda()
+    b = torch.randn(n, n, generator=g).bfloat16().cuda()
+    c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
+
+    def run():
+        torch.matmul(a, b, out=c)
+
+    return dict(run=run, work=2 * n ** 3, bound="mfma", kernel="Cijk",
+                config={"m": n, "n": n, "k": n, "dtype": "bf16"}, cpu=None)
+
+
 def _wl_hbm_stream(reads):
     """The HBM ceiling the bandwidth-bound ops can reach: `kcr_hbm_stream_probe`,
     the gated kernel's memory shape with no arithmetic. reads=1 copies the
@@ -372,8 +388,9 @@ WORKLOADS = {
     "hbm_stream_1to1": _wl_hbm_stream(1),
     "hbm_stream_2to1": _wl_hbm_stream(2),
     "hbm_copy": wl_hbm_copy,
+    "gemm_ceiling": wl_gemm_ceiling,
 }
-DEFAULT_ORDER = [n for n in WORKLOADS if n != "hbm_copy"]
+DEFAULT_ORDER = [n for n in WORKLOADS if n not in ("hbm_copy", "gemm_ceiling")]
 # Ops whose CPU baseline is timed in every default run (bounded samples).
 CPU_OPS = ("fa_fwd_causal", "fa_fwd_config1", "rms_norm", "silu_and_mul")
 
