@@ -491,20 +491,25 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         qo = rem / p.heads;
         const int idx = rem - qo * p.heads;
         head = (idx % p.kv_heads) * p.gqa + idx / p.kv_heads;
+    } else if (p.xcd_groups) {
+        // Group-major per XCD (blocks go to XCD blockIdx % 8): each XCD runs
+        // the query tiles of one (batch, KV head) group, longest first over its
+        // query heads, before the next group, so one group's K/V tiles are live
+        // in the XCD's L2 at a time.
+        const int xcd = bid & 7;
+        const int k = bid >> 3;
+        const int per_group = p.q_blocks * p.gqa;
+        const int gl = k / per_group;
+        const int t = k - gl * per_group;
+        qo = t / p.gqa;
+        const int j = t - qo * p.gqa;
+        const int bh = (gl * 8 + xcd) * p.gqa + j;
+        b = bh / p.heads;
+        head = bh - b * p.heads;
     } else {
         const int per_tile = p.batch * p.heads;
         qo = bid / per_tile;
-        const int rem = bid - qo * per_tile;
-        int bh;
-        if (p.xcd_groups) {
-            const int xcd = rem & 7;
-            const int rr = rem >> 3;
-            const int j = rr % p.gqa;
-            const int g = (rr / p.gqa) * 8 + xcd;
-            bh = g * p.gqa + j;
-        } else {
-            bh = rem;
-        }
+        const int bh = bid - qo * per_tile;
         b = bh / p.heads;
         head = bh - b * p.heads;
     }
