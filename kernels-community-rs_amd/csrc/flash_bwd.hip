@@ -53,6 +53,7 @@ struct BwdParams {
     int32_t window_left, window_right;
     int32_t blocks_per_seq;  // key blocks (dkv) or query blocks (dq) per (batch, head)
     int32_t seq_major;       // varlen v2 kernels: sequence-major block order
+    int32_t pair_tiles;      // dK/dV v2 kernel (paired instance): each block takes key tiles t and per - 1 - t
     int32_t alibi_b, alibi_causal;
     float scale_log2;
     float tanh_scale;
@@ -819,7 +820,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     }
 }
 
-template <typename T, int D, int NW, bool VARLEN, bool DROPOUT>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool PAIRED>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const BwdParams p) {
     // D = 128: the dK and dV accumulators (128 registers) and K (32) leave no
     // room for V in registers at 2 waves per SIMD, so V is staged once in LDS
@@ -847,7 +848,32 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
     // Tile-major order: the key tiles that see the most causal queries start
     // first across the whole grid; one (batch, KV head) keeps one XCD.
     int b, kvh, kbi;
-    if (p.seq_major) {
+    int kbi2 = -1;  // the second key tile of a paired block
+    if constexpr (PAIRED) {
+        // Masked dense grids: block pr of a (batch, KV head) group takes key
+        // tiles pr and per - 1 - pr, whose causal work adds up to the same for
+        // every block. With equal blocks the grid runs group-major per XCD
+        // (blocks go to XCD blockIdx % 8): one group's Q / dO tiles are read by
+        // the blocks of one XCD at a time.
+        const int per = p.blocks_per_seq;
+        const int npairs = (per + 1) / 2;
+        int g, pr;
+        if ((p.batch * p.kv_heads) % 8 == 0) {
+            const int xcd = static_cast<int>(blockIdx.x) & 7;
+            const int k = static_cast<int>(blockIdx.x) >> 3;
+            const int gl = k / npairs;
+            pr = k - gl * npairs;
+            g = gl * 8 + xcd;
+        } else {
+            g = static_cast<int>(blockIdx.x) / npairs;
+            pr = static_cast<int>(blockIdx.x) - g * npairs;
+        }
+        b = g / p.kv_heads;
+        kvh = g - b * p.kv_heads;
+        kbi = pr;
+        kbi2 = per - 1 - pr;
+        if (kbi2 == kbi) kbi2 = -1;
+    } else if (p.seq_major) {
         // Sequence-major (see the dQ kernel): key tiles of one sequence together.
         const int per = p.blocks_per_seq;
         b = blockIdx.x / (per * p.kv_heads);
@@ -866,285 +892,297 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
     if constexpr (DROPOUT) drop = dropout_state(p);
     if (!sb.ok) return;
     const int sq = sb.sq, sk = sb.sk;
-    const int key0 = kbi * BK;
-    if (key0 >= sk) return;
-    const int off = sk - sq;
-    const int wl = p.window_left, wr = p.window_right;
+    // One key tile, or two for a paired block (the body is inlined once per
+    // tile, so the two copies' registers do not overlap); the tile loop's last
+    // barrier orders the second tile's V and Q / dO staging after every read
+    // of the first.
+    auto key_tile = [&](const int kt) __attribute__((always_inline)) {
+        const int key0 = kt * BK;
+        if (key0 >= sk) return;
+        const int off = sk - sq;
+        const int wl = p.window_left, wr = p.window_right;
 
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (VARLEN ? sb.k_off * p.k_s : b * p.k_b) + kvh * p.k_h;
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (VARLEN ? sb.k_off * p.v_s : b * p.v_b) + kvh * p.v_h;
+        const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (VARLEN ? sb.k_off * p.k_s : b * p.k_b) + kvh * p.k_h;
+        const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (VARLEN ? sb.k_off * p.v_s : b * p.v_b) + kvh * p.v_h;
 
-    // This wave's 32 keys: K (and V) rows as B operands of S = Q K^T, dP = dO V^T.
-    const int my_key = key0 + 32 * wave + l32;
-    u32x4 kf[KS];
-    u32x4 vf[V_LDS ? 1 : KS];
+        // This wave's 32 keys: K (and V) rows as B operands of S = Q K^T, dP = dO V^T.
+        const int my_key = key0 + 32 * wave + l32;
+        u32x4 kf[KS];
+        u32x4 vf[V_LDS ? 1 : KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int d0 = 16 * ks + 8 * hh;
-        const bool ok = my_key < sk;
-        kf[ks] = ok ? *reinterpret_cast<const u32x4*>(kbase + my_key * p.k_s + d0) : u32x4{0, 0, 0, 0};
-        if constexpr (!V_LDS) {
-            vf[ks] = ok ? *reinterpret_cast<const u32x4*>(vbase + my_key * p.v_s + d0) : u32x4{0, 0, 0, 0};
-        }
-    }
-    if constexpr (V_LDS) {
-        copy_rows_dma<D, NW, BK>(vbase + static_cast<int64_t>(key0) * p.v_s, p.v_s, sk - key0, v_lds, wave, lane);
-    }
-    f32x16 dk[DB], dv[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        dk[db] = f32x16{};
-        dv[db] = f32x16{};
-    }
-
-    // Query rows that can see some key of this block.
-    const int key_last = min(key0 + BK, sk) - 1;
-    int q_begin = 0;
-    if (wr >= 0) q_begin = max(0, key0 - off - wr);
-    q_begin = (q_begin / BQ) * BQ;
-    int q_end = sq;
-    if (wl >= 0) q_end = max(0, min(sq, key_last - off + wl + 1));
-    const int nqb = q_begin < q_end ? (q_end - q_begin + BQ - 1) / BQ : 0;
-    // (query tile, query head of the group) pairs, last query tile first: the
-    // key blocks of one (batch, KV head) run on one XCD and all end at the last
-    // query tile, so walking the tiles downward keeps them reading the same
-    // Q / dO tiles at the same time (shared through L2).
-    const int gqa = p.gqa;
-    const int ntiles = nqb * gqa;
-    const float c = p.scale_log2;
-
-    // Tile t is query tile nqb - 1 - t / gqa (counted from q_begin) of query
-    // head kvh * gqa + t % gqa. The copies walk that order with a cursor of row
-    // pointers stepped per tile (no division or 64-bit multiply per tile).
-    struct Cursor {
-        int j, qb;  // head within the group, first query row of the tile
-        const uint16_t* q;
-        const uint16_t* dout;
-        const float* lse;
-        const float* delta;
-    };
-    const int qb_last = q_begin + (nqb - 1) * BQ;
-    Cursor cur;
-    {
-        const int head0 = kvh * gqa;
-        cur.j = 0;
-        cur.qb = qb_last;
-        cur.q = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head0 * p.q_h +
-                static_cast<int64_t>(qb_last) * p.q_s;
-        cur.dout = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) +
-                   head0 * p.do_h + static_cast<int64_t>(qb_last) * p.do_s;
-        cur.lse = p.lse + (VARLEN ? 0 : b * p.lse_b) + head0 * p.lse_h + sb.lse_row0 + qb_last;
-        cur.delta = p.delta + (VARLEN ? 0 : b * p.delta_b) + head0 * p.delta_h + sb.delta_row0 + qb_last;
-    }
-    // Steps when the head index wraps: back to the group's first head, one
-    // query tile down.
-    const int64_t q_wrap = -static_cast<int64_t>(gqa) * p.q_h - static_cast<int64_t>(BQ) * p.q_s;
-    const int64_t do_wrap = -static_cast<int64_t>(gqa) * p.do_h - static_cast<int64_t>(BQ) * p.do_s;
-    const int64_t lse_wrap = -static_cast<int64_t>(gqa) * p.lse_h - BQ;
-    const int64_t delta_wrap = -static_cast<int64_t>(gqa) * p.delta_h - BQ;
-    auto advance = [&](Cursor& c) {
-        ++c.j;
-        c.q += p.q_h;
-        c.dout += p.do_h;
-        c.lse += p.lse_h;
-        c.delta += p.delta_h;
-        if (c.j == gqa) {
-            c.j = 0;
-            c.qb -= BQ;
-            c.q += q_wrap;
-            c.dout += do_wrap;
-            c.lse += lse_wrap;
-            c.delta += delta_wrap;
-        }
-    };
-    auto copy_tile = [&](const Cursor& c, int stage) {
-        copy_rows_dma<D, NW, BQ>(c.q, p.q_s, sq - c.qb, q_lds + stage * TILE, wave, lane);
-        copy_rows_dma<D, NW, BQ>(c.dout, p.do_s, sq - c.qb, do_lds + stage * TILE, wave, lane);
-        // Rows past the sequence read LSE 0 and delta 0; their Q and dO rows are
-        // zero, so they add nothing to dK and dV.
-        const uint32_t rows = static_cast<uint32_t>(max(0, min(sq - c.qb, BQ)));
-        if (wave == 0) {
-            dma_lds4(rsrc_words(c.lse, rows * 4u), lds_addr(lse_lds + stage * 64), lane * 4u);
-        } else if (wave == 1) {
-            dma_lds4(rsrc_words(c.delta, rows * 4u), lds_addr(dl_lds + stage * 64), lane * 4u);
-        }
-    };
-    if (ntiles > 0) copy_tile(cur, 0);
-    wait_vmem();
-    __syncthreads();
-    int tj = 0, qb = qb_last;  // the computed tile's head index and first row
-
-    for (int t = 0; t < ntiles; ++t) {
-        tl.refresh();
-        const int stage = t & 1;
-        const uint16_t* ql = q_lds + stage * TILE;
-        const uint16_t* dl = do_lds + stage * TILE;
-        const float* lsl = lse_lds + stage * 64;
-        const float* dll = dl_lds + stage * 64;
-        if (t + 1 < ntiles) {
-            advance(cur);
-            copy_tile(cur, stage ^ 1);
-        }
-
-        const bool need_mask = (key0 + BK > sk) || (wr >= 0 && key0 + BK - 1 > qb + off + wr) ||
-                               (wl >= 0 && key0 < qb + BQ - 1 + off - wl);
-#pragma unroll
-        for (int qc = 0; qc < NQC; ++qc) {
-            // S = Q K^T and dP = dO V^T; the operands of k-step ks + 1 are read
-            // while the MFMAs of k-step ks run.
-            f32x16 s = f32x16{}, dp = f32x16{};
-            {
-                constexpr int NR = V_LDS ? 3 : 2;
-                auto rd = [&](auto ic, u32x4 (&r)[NR]) __attribute__((always_inline)) {
-                    constexpr int ks = decltype(ic)::value;
-                    r[0] = tl.rm(ql, qc, ks);
-                    r[1] = tl.rm(dl, qc, ks);
-                    if constexpr (V_LDS) r[2] = tl.rm(v_lds, wave, ks);
-                };
-                u32x4 ra[2][NR];
-                rd(std::integral_constant<int, 0>{}, ra[0]);
-                __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-                static_for<0, KS>([&](auto ic) __attribute__((always_inline)) {
-                    constexpr int ks = decltype(ic)::value;
-                    if constexpr (ks + 1 < KS) {
-                        rd(std::integral_constant<int, ks + 1>{}, ra[(ks + 1) & 1]);
-                        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-                    }
-                    const u32x4(&r)[NR] = ra[ks & 1];
-                    s = mfma32<T>(r[0], kf[ks], s);
-                    if constexpr (V_LDS) {
-                        dp = mfma32<T>(r[1], r[2], dp);
-                    } else {
-                        dp = mfma32<T>(r[1], vf[ks], dp);
-                    }
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                });
-            }
-            u32x4 pP[2], pS[2];
-            float pv[16], dsv[16];
-            uint32_t keep_bits = 0xFFFFu;
-            if constexpr (DROPOUT) {
-                keep_bits = keep_bits_key_lane_shared(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + tj),
-                                               static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh);
-            }
-            // The mask test is hoisted out of the element loop: one branch per
-            // tile instead of a scalar branch per element.
-            auto p_ds = [&](auto mask_tag) __attribute__((always_inline)) {
-                constexpr bool MASK = decltype(mask_tag)::value;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int qloc = 32 * qc + 8 * g + 4 * hh;
-                    const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
-                    const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = 4 * g + e;
-                        float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
-                        if constexpr (MASK) {
-                            const int row = qb + qloc + e;
-                            const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
-                                                (wl >= 0 & my_key < row + off - wl);
-                            pr = masked ? 0.0f : pr;
-                        }
-                        const bool kept = ((keep_bits >> r) & 1u) != 0u;
-                        pv[r] = kept ? pr : 0.0f;
-                        dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
-                    }
-                }
-            };
-            if constexpr (DROPOUT) {
-                // The dropout kernel keeps the per-element test inline: through
-                // the lambda it spills.
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int qloc = 32 * qc + 8 * g + 4 * hh;
-                    const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
-                    const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = 4 * g + e;
-                        float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
-                        if (need_mask) {
-                            const int row = qb + qloc + e;
-                            const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
-                                                (wl >= 0 & my_key < row + off - wl);
-                            pr = masked ? 0.0f : pr;
-                        }
-                        const bool kept = ((keep_bits >> r) & 1u) != 0u;
-                        pv[r] = kept ? pr : 0.0f;
-                        dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
-                    }
-                }
-            } else if (need_mask) {
-                p_ds(std::true_type{});
-            } else {
-                p_ds(std::false_type{});
-            }
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2) {
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    pP[t2][w] = pack2<T>(pv[8 * t2 + 2 * w], pv[8 * t2 + 2 * w + 1]);
-                    pS[t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
-                }
-            }
-            // dV^T += dO^T P and dK^T += Q^T dS (transposed reads of the query
-            // tiles), step i = (db, t2) with the next step's operands in flight.
-            {
-                auto rd = [&](auto ic, u32x4 (&r)[2]) __attribute__((always_inline)) {
-                    constexpr int i = decltype(ic)::value;
-                    r[0] = tl.tr(dl, i >> 1, 2 * qc + (i & 1));
-                    r[1] = tl.tr(ql, i >> 1, 2 * qc + (i & 1));
-                };
-                u32x4 rb[2][2];
-                rd(std::integral_constant<int, 0>{}, rb[0]);
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                static_for<0, 2 * DB>([&](auto ic) __attribute__((always_inline)) {
-                    constexpr int i = decltype(ic)::value;
-                    constexpr int db = i >> 1, t2 = i & 1;
-                    if constexpr (i + 1 < 2 * DB) {
-                        rd(std::integral_constant<int, i + 1>{}, rb[(i + 1) & 1]);
-                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                    }
-                    const u32x4(&r)[2] = rb[i & 1];
-                    dv[db] = mfma32<T>(r[0], pP[t2], dv[db]);
-                    dk[db] = mfma32<T>(r[1], pS[t2], dk[db]);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                });
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = 16 * ks + 8 * hh;
+            const bool ok = my_key < sk;
+            kf[ks] = ok ? *reinterpret_cast<const u32x4*>(kbase + my_key * p.k_s + d0) : u32x4{0, 0, 0, 0};
+            if constexpr (!V_LDS) {
+                vf[ks] = ok ? *reinterpret_cast<const u32x4*>(vbase + my_key * p.v_s + d0) : u32x4{0, 0, 0, 0};
             }
         }
-        if (++tj == gqa) {
-            tj = 0;
-            qb -= BQ;
+        if constexpr (V_LDS) {
+            copy_rows_dma<D, NW, BK>(vbase + static_cast<int64_t>(key0) * p.v_s, p.v_s, sk - key0, v_lds, wave, lane);
         }
-        wait_vmem();
-        __syncthreads();
-    }
-
-    if (my_key < sk) {
-        uint16_t* dkrow = static_cast<uint16_t*>(p.dk) + (VARLEN ? sb.k_off * p.dk_s : b * p.dk_b) +
-                          kvh * p.dk_h + my_key * p.dk_s;
-        uint16_t* dvrow = static_cast<uint16_t*>(p.dv) + (VARLEN ? sb.k_off * p.dv_s : b * p.dv_b) +
-                          kvh * p.dv_h + my_key * p.dv_s;
-        const float gs = p.grad_scale;
+        f32x16 dk[DB], dv[DB];
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
+            dk[db] = f32x16{};
+            dv[db] = f32x16{};
+        }
+
+        // Query rows that can see some key of this block.
+        const int key_last = min(key0 + BK, sk) - 1;
+        int q_begin = 0;
+        if (wr >= 0) q_begin = max(0, key0 - off - wr);
+        q_begin = (q_begin / BQ) * BQ;
+        int q_end = sq;
+        if (wl >= 0) q_end = max(0, min(sq, key_last - off + wl + 1));
+        const int nqb = q_begin < q_end ? (q_end - q_begin + BQ - 1) / BQ : 0;
+        // (query tile, query head of the group) pairs, last query tile first: the
+        // key blocks of one (batch, KV head) run on one XCD and all end at the last
+        // query tile, so walking the tiles downward keeps them reading the same
+        // Q / dO tiles at the same time (shared through L2).
+        const int gqa = p.gqa;
+        const int ntiles = nqb * gqa;
+        const float c = p.scale_log2;
+
+        // Tile t is query tile nqb - 1 - t / gqa (counted from q_begin) of query
+        // head kvh * gqa + t % gqa. The copies walk that order with a cursor of row
+        // pointers stepped per tile (no division or 64-bit multiply per tile).
+        struct Cursor {
+            int j, qb;  // head within the group, first query row of the tile
+            const uint16_t* q;
+            const uint16_t* dout;
+            const float* lse;
+            const float* delta;
+        };
+        const int qb_last = q_begin + (nqb - 1) * BQ;
+        Cursor cur;
+        {
+            const int head0 = kvh * gqa;
+            cur.j = 0;
+            cur.qb = qb_last;
+            cur.q = static_cast<const uint16_t*>(p.q) + (VARLEN ? sb.q_off * p.q_s : b * p.q_b) + head0 * p.q_h +
+                    static_cast<int64_t>(qb_last) * p.q_s;
+            cur.dout = static_cast<const uint16_t*>(p.dout) + (VARLEN ? sb.q_off * p.do_s : b * p.do_b) +
+                       head0 * p.do_h + static_cast<int64_t>(qb_last) * p.do_s;
+            cur.lse = p.lse + (VARLEN ? 0 : b * p.lse_b) + head0 * p.lse_h + sb.lse_row0 + qb_last;
+            cur.delta = p.delta + (VARLEN ? 0 : b * p.delta_b) + head0 * p.delta_h + sb.delta_row0 + qb_last;
+        }
+        // Steps when the head index wraps: back to the group's first head, one
+        // query tile down.
+        const int64_t q_wrap = -static_cast<int64_t>(gqa) * p.q_h - static_cast<int64_t>(BQ) * p.q_s;
+        const int64_t do_wrap = -static_cast<int64_t>(gqa) * p.do_h - static_cast<int64_t>(BQ) * p.do_s;
+        const int64_t lse_wrap = -static_cast<int64_t>(gqa) * p.lse_h - BQ;
+        const int64_t delta_wrap = -static_cast<int64_t>(gqa) * p.delta_h - BQ;
+        auto advance = [&](Cursor& c) {
+            ++c.j;
+            c.q += p.q_h;
+            c.dout += p.do_h;
+            c.lse += p.lse_h;
+            c.delta += p.delta_h;
+            if (c.j == gqa) {
+                c.j = 0;
+                c.qb -= BQ;
+                c.q += q_wrap;
+                c.dout += do_wrap;
+                c.lse += lse_wrap;
+                c.delta += delta_wrap;
+            }
+        };
+        auto copy_tile = [&](const Cursor& c, int stage) {
+            copy_rows_dma<D, NW, BQ>(c.q, p.q_s, sq - c.qb, q_lds + stage * TILE, wave, lane);
+            copy_rows_dma<D, NW, BQ>(c.dout, p.do_s, sq - c.qb, do_lds + stage * TILE, wave, lane);
+            // Rows past the sequence read LSE 0 and delta 0; their Q and dO rows are
+            // zero, so they add nothing to dK and dV.
+            const uint32_t rows = static_cast<uint32_t>(max(0, min(sq - c.qb, BQ)));
+            if (wave == 0) {
+                dma_lds4(rsrc_words(c.lse, rows * 4u), lds_addr(lse_lds + stage * 64), lane * 4u);
+            } else if (wave == 1) {
+                dma_lds4(rsrc_words(c.delta, rows * 4u), lds_addr(dl_lds + stage * 64), lane * 4u);
+            }
+        };
+        if (ntiles > 0) copy_tile(cur, 0);
+        wait_vmem();
+        __syncthreads();
+        int tj = 0, qb = qb_last;  // the computed tile's head index and first row
+
+        for (int t = 0; t < ntiles; ++t) {
+            tl.refresh();
+            const int stage = t & 1;
+            const uint16_t* ql = q_lds + stage * TILE;
+            const uint16_t* dl = do_lds + stage * TILE;
+            const float* lsl = lse_lds + stage * 64;
+            const float* dll = dl_lds + stage * 64;
+            if (t + 1 < ntiles) {
+                advance(cur);
+                copy_tile(cur, stage ^ 1);
+            }
+
+            const bool need_mask = (key0 + BK > sk) || (wr >= 0 && key0 + BK - 1 > qb + off + wr) ||
+                                   (wl >= 0 && key0 < qb + BQ - 1 + off - wl);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = 32 * db + 8 * g + 4 * hh;
-                uint2 a, cc;
-                a.x = pack2<T>(dk[db][4 * g] * gs, dk[db][4 * g + 1] * gs);
-                a.y = pack2<T>(dk[db][4 * g + 2] * gs, dk[db][4 * g + 3] * gs);
-                cc.x = pack2<T>(dv[db][4 * g] * p.inv_keep, dv[db][4 * g + 1] * p.inv_keep);
-                cc.y = pack2<T>(dv[db][4 * g + 2] * p.inv_keep, dv[db][4 * g + 3] * p.inv_keep);
-                *reinterpret_cast<uint2*>(dkrow + d) = a;
-                *reinterpret_cast<uint2*>(dvrow + d) = cc;
+            for (int qc = 0; qc < NQC; ++qc) {
+                // S = Q K^T and dP = dO V^T; the operands of k-step ks + 1 are read
+                // while the MFMAs of k-step ks run.
+                f32x16 s = f32x16{}, dp = f32x16{};
+                {
+                    constexpr int NR = V_LDS ? 3 : 2;
+                    auto rd = [&](auto ic, u32x4 (&r)[NR]) __attribute__((always_inline)) {
+                        constexpr int ks = decltype(ic)::value;
+                        r[0] = tl.rm(ql, qc, ks);
+                        r[1] = tl.rm(dl, qc, ks);
+                        if constexpr (V_LDS) r[2] = tl.rm(v_lds, wave, ks);
+                    };
+                    u32x4 ra[2][NR];
+                    rd(std::integral_constant<int, 0>{}, ra[0]);
+                    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+                    static_for<0, KS>([&](auto ic) __attribute__((always_inline)) {
+                        constexpr int ks = decltype(ic)::value;
+                        if constexpr (ks + 1 < KS) {
+                            rd(std::integral_constant<int, ks + 1>{}, ra[(ks + 1) & 1]);
+                            __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+                        }
+                        const u32x4(&r)[NR] = ra[ks & 1];
+                        s = mfma32<T>(r[0], kf[ks], s);
+                        if constexpr (V_LDS) {
+                            dp = mfma32<T>(r[1], r[2], dp);
+                        } else {
+                            dp = mfma32<T>(r[1], vf[ks], dp);
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    });
+                }
+                u32x4 pP[2], pS[2];
+                float pv[16], dsv[16];
+                uint32_t keep_bits = 0xFFFFu;
+                if constexpr (DROPOUT) {
+                    keep_bits = keep_bits_key_lane_shared(drop, static_cast<uint32_t>(b * p.heads + kvh * gqa + tj),
+                                                   static_cast<uint32_t>(qb + 32 * qc), static_cast<uint32_t>(my_key), hh);
+                }
+                // The mask test is hoisted out of the element loop: one branch per
+                // tile instead of a scalar branch per element.
+                auto p_ds = [&](auto mask_tag) __attribute__((always_inline)) {
+                    constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int qloc = 32 * qc + 8 * g + 4 * hh;
+                        const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
+                        const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
+                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = 4 * g + e;
+                            float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                            if constexpr (MASK) {
+                                const int row = qb + qloc + e;
+                                const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
+                                                    (wl >= 0 & my_key < row + off - wl);
+                                pr = masked ? 0.0f : pr;
+                            }
+                            const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                            pv[r] = kept ? pr : 0.0f;
+                            dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
+                        }
+                    }
+                };
+                if constexpr (DROPOUT) {
+                    // The dropout kernel keeps the per-element test inline: through
+                    // the lambda it spills.
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int qloc = 32 * qc + 8 * g + 4 * hh;
+                        const float4 l4 = *reinterpret_cast<const float4*>(lsl + qloc);
+                        const float4 d4 = *reinterpret_cast<const float4*>(dll + qloc);
+                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = 4 * g + e;
+                            float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                            if (need_mask) {
+                                const int row = qb + qloc + e;
+                                const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
+                                                    (wl >= 0 & my_key < row + off - wl);
+                                pr = masked ? 0.0f : pr;
+                            }
+                            const bool kept = ((keep_bits >> r) & 1u) != 0u;
+                            pv[r] = kept ? pr : 0.0f;
+                            dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
+                        }
+                    }
+                } else if (need_mask) {
+                    p_ds(std::true_type{});
+                } else {
+                    p_ds(std::false_type{});
+                }
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        pP[t2][w] = pack2<T>(pv[8 * t2 + 2 * w], pv[8 * t2 + 2 * w + 1]);
+                        pS[t2][w] = pack2<T>(dsv[8 * t2 + 2 * w], dsv[8 * t2 + 2 * w + 1]);
+                    }
+                }
+                // dV^T += dO^T P and dK^T += Q^T dS (transposed reads of the query
+                // tiles), step i = (db, t2) with the next step's operands in flight.
+                {
+                    auto rd = [&](auto ic, u32x4 (&r)[2]) __attribute__((always_inline)) {
+                        constexpr int i = decltype(ic)::value;
+                        r[0] = tl.tr(dl, i >> 1, 2 * qc + (i & 1));
+                        r[1] = tl.tr(ql, i >> 1, 2 * qc + (i & 1));
+                    };
+                    u32x4 rb[2][2];
+                    rd(std::integral_constant<int, 0>{}, rb[0]);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                    static_for<0, 2 * DB>([&](auto ic) __attribute__((always_inline)) {
+                        constexpr int i = decltype(ic)::value;
+                        constexpr int db = i >> 1, t2 = i & 1;
+                        if constexpr (i + 1 < 2 * DB) {
+                            rd(std::integral_constant<int, i + 1>{}, rb[(i + 1) & 1]);
+                            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                        }
+                        const u32x4(&r)[2] = rb[i & 1];
+                        dv[db] = mfma32<T>(r[0], pP[t2], dv[db]);
+                        dk[db] = mfma32<T>(r[1], pS[t2], dk[db]);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    });
+                }
+            }
+            if (++tj == gqa) {
+                tj = 0;
+                qb -= BQ;
+            }
+            wait_vmem();
+            __syncthreads();
+        }
+
+        if (my_key < sk) {
+            uint16_t* dkrow = static_cast<uint16_t*>(p.dk) + (VARLEN ? sb.k_off * p.dk_s : b * p.dk_b) +
+                              kvh * p.dk_h + my_key * p.dk_s;
+            uint16_t* dvrow = static_cast<uint16_t*>(p.dv) + (VARLEN ? sb.k_off * p.dv_s : b * p.dv_b) +
+                              kvh * p.dv_h + my_key * p.dv_s;
+            const float gs = p.grad_scale;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * db + 8 * g + 4 * hh;
+                    uint2 a, cc;
+                    a.x = pack2<T>(dk[db][4 * g] * gs, dk[db][4 * g + 1] * gs);
+                    a.y = pack2<T>(dk[db][4 * g + 2] * gs, dk[db][4 * g + 3] * gs);
+                    cc.x = pack2<T>(dv[db][4 * g] * p.inv_keep, dv[db][4 * g + 1] * p.inv_keep);
+                    cc.y = pack2<T>(dv[db][4 * g + 2] * p.inv_keep, dv[db][4 * g + 3] * p.inv_keep);
+                    *reinterpret_cast<uint2*>(dkrow + d) = a;
+                    *reinterpret_cast<uint2*>(dvrow + d) = cc;
+                }
             }
         }
+    };
+    key_tile(kbi);
+    // Only the paired instance carries a second inlined copy of the body
+    // (the dropout kernel's would not fit the registers of two waves per SIMD).
+    if constexpr (PAIRED) {
+        if (kbi2 >= 0) key_tile(kbi2);
     }
 }
 
@@ -1183,9 +1221,20 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
     if (want_kv) {
         constexpr int BK = 32 * DKV_WAVES;
         prm.blocks_per_seq = (prm.seqlen_k + BK - 1) / BK;
-        const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.kv_heads;
+        // Paired blocks take two key tiles each (see the kernel).
+        const int64_t per_group = prm.pair_tiles ? (prm.blocks_per_seq + 1) / 2 : prm.blocks_per_seq;
+        const int64_t blocks = per_group * prm.batch * prm.kv_heads;
         if (blocks > 0) {
-            flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN, DROPOUT><<<static_cast<unsigned>(blocks), DKV_WAVES * 64, 0, s>>>(prm);
+            const unsigned grid = static_cast<unsigned>(blocks);
+            if constexpr (!VARLEN && !DROPOUT) {
+                if (prm.pair_tiles) {
+                    flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, false, false, true><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
+                } else {
+                    flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, false, false, false><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
+                }
+            } else {
+                flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN, DROPOUT, false><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
+            }
             check_launch("launch flash_bwd_dkv");
         }
     }
@@ -1213,6 +1262,7 @@ void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
             // concurrent blocks then share one sequence's tiles in L2. Masked
             // dense grids keep the tile-major, longest-first order.
             prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
+            prm.pair_tiles = (prm.seq_major || prm.drop_threshold < 255) ? 0 : 1;
             if (prm.drop_threshold < 255) {
                 launch_bwd_v2<T, D, VARLEN, 4, 4, true>(prm, want_q, want_kv, s);
             } else {
