@@ -351,8 +351,9 @@ __global__ void __launch_bounds__(kThreads) activation_vec(u32x4* __restrict__ o
 // 16384 x 28672 bf16): a grid that covers the input in one pass (every block
 // one iteration, blocks dispatched as CUs free up) streams at 6.35-6.39 TB/s;
 // capping the grid at 1, 4 or 16 blocks per CU and looping gave 5.54, 5.79
-// and 6.06 TB/s: the dispatcher's dynamic balance across CUs is worth more
-// than the 128 KB table copy each block makes from L2. The element-wise
+// and 6.06 TB/s, and 8 vectors per thread (half the blocks, one pass) 6.0:
+// the dispatcher's dynamic balance across CUs is worth more than the 128 KB
+// table copy each block makes from L2. The element-wise
 // kernels (one input) run best with U = 2 and at most 24 blocks per CU
 // (6.12 TB/s against 5.65 for one pass at U = 4).
 constexpr int kLutThreads = 1024;
