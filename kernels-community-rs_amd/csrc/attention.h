@@ -132,6 +132,7 @@ struct FwdParams {
     // Split-KV (tiled varlen kernel): n_splits > 1 writes per-split fp32 partials
     // o_part [n_splits, H, Tq, D] (normalised) and lse_part [n_splits, H, Tq].
     int32_t n_splits;
+    int32_t scored;              // tiled kernels: softcap and / or ALiBi score transform
     float* o_part;
     float* lse_part;
     // Batched cache queries: rows_per_seq > 0 means q/o [B, rows_per_seq, H, D]

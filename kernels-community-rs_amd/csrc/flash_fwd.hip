@@ -452,9 +452,11 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // packed in place into the B operand of the PV MFMA. Two LDS stages, the next
 // tile's copy in flight during the current tile, one barrier per tile. STREAM:
 // every K/V tile is read by this block only (cache decode with grouped rows),
-// so the copies are non-temporal.
+// so the copies are non-temporal. SCORED: the scores are transformed before
+// the softmax (softcap tanh and / or the ALiBi bias, in log2 units), which
+// then runs with the scale already applied.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool VARLEN, bool DROPOUT, bool STREAM>
+template <typename T, int D, bool VARLEN, bool DROPOUT, bool STREAM, bool SCORED = false>
 __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams p) {
     constexpr int NW = 4;
     constexpr int BN = kBN;
@@ -588,7 +590,13 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         qf[ks] = row < sq ? *reinterpret_cast<const u32x4*>(qbase + row * p.q_s + 16 * ks + 8 * hh)
                           : u32x4{0, 0, 0, 0};
     }
-    const float c = p.scale_log2;
+    // Fast path: exp2(s * c - m) with the scale folded into one FMA; scored
+    // tiles carry the scale (and bias) in the scores themselves.
+    const float c = SCORED ? 1.0f : p.scale_log2;
+    [[maybe_unused]] float slope_log2 = 0.0f;
+    if constexpr (SCORED) {
+        if (p.alibi) slope_log2 = p.alibi[b * p.alibi_b + head] * kLog2e;
+    }
 
     f32x16 o[DB];
 #pragma unroll
@@ -664,6 +672,24 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
             });
         }
 
+        if constexpr (SCORED) {
+            // The general kernel's score transform (same operations, same order).
+            const bool cap = p.tanh_scale > 0.0f;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    float x = s[sub][r];
+                    x = cap ? tanhf(x * p.tanh_scale) * p.scale_eff_log2 : x * p.scale_log2;
+                    if (p.alibi) {
+                        x += p.alibi_causal ? slope_log2 * static_cast<float>(col)
+                                            : -slope_log2 * fabsf(static_cast<float>(row + off - col));
+                    }
+                    s[sub][r] = x;
+                }
+            }
+        }
         const bool need_mask = (kb + BN > sk) || (wr >= 0 && kb + BN - 1 > row0 + off + wr) ||
                                (wl >= 0 && kb < last_row + off - wl);
         if (need_mask) {
@@ -1233,7 +1259,13 @@ void launch_tiled(FwdParams& prm, hipStream_t s) {
     // Sequence-major order for packed sequences and unmasked grids (blocks of
     // equal work); masked dense grids keep the longest-first tile-major order.
     prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
-    if (prm.drop_threshold < 255) {
+    if (prm.scored) {
+        if (prm.drop_threshold < 255) {
+            flash_fwd_tiled_kernel<T, D, VARLEN, true, false, true><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+        } else {
+            flash_fwd_tiled_kernel<T, D, VARLEN, false, false, true><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
+        }
+    } else if (prm.drop_threshold < 255) {
         flash_fwd_tiled_kernel<T, D, VARLEN, true, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(prm);
     } else if constexpr (VARLEN) {
         if (prm.cache_mode && prm.q_blocks == 1 && prm.heads == prm.kv_heads) {
@@ -1271,7 +1303,7 @@ void launch_d(FwdParams& prm, bool general, hipStream_t s) {
             // windowed, dropout, packed and D = 64 grids).
             if constexpr (D == 128 && !VARLEN) {
                 if (prm.window_left < 0 && prm.window_right < 0 && prm.drop_threshold == 255 &&
-                    prm.n_splits <= 1) {
+                    prm.n_splits <= 1 && !prm.scored) {
                     return launch_pp<T, D, VARLEN>(prm, s);
                 }
             }
@@ -1548,9 +1580,14 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
         prm.tanh_scale = opt.tanh_scale;
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
         set_dropout(prm, drop);
-        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
+        // Softcap / ALiBi run in the tiled kernels' scored variant; head sizes
+        // the tiles do not cover and non-positive plain scales take the general
+        // kernel.
+        prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
+        const bool general = D % 32 != 0 || (D != 64 && D != 128 && prm.scored) ||
+                             (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(D);
-        const int64_t splits = (general || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
+        const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
                                    ? 1
                                    : dense_splits(B, H, Sq, Sk, compute_units());
         // The probabilities read the final LSE (after any merge).
@@ -1700,9 +1737,14 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
         prm.tanh_scale = opt.tanh_scale;
         prm.scale_eff_log2 = opt.scale_eff * kLog2e;
         set_dropout(prm, drop);
-        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
+        // Softcap / ALiBi run in the tiled kernels' scored variant; head sizes
+        // the tiles do not cover and non-positive plain scales take the general
+        // kernel.
+        prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
+        const bool general = D % 32 != 0 || (D != 64 && D != 128 && prm.scored) ||
+                             (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(D);
-        const int64_t splits = (general || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
+        const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
                                    ? 1
                                    : dense_splits(batch, H, max_seqlen_q, max_seqlen_k, compute_units());
         if (splits <= 1) {
@@ -1917,6 +1959,7 @@ void fwd_kvcache_impl(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_t
             prm.k_page = kcache->strides[0];
             prm.v_page = vcache->strides[0];
         }
+        // Cached attention with softcap / ALiBi stays on the general kernel.
         const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
         const int bucket = bucket_for(D);
         const bool tiled = !general && (bucket == 64 || bucket == 128);
