@@ -118,6 +118,21 @@ __device__ __forceinline__ float bwd_score(const BwdParams& p, float raw, int ro
     }
 }
 
+// P = 2^(score - lse) of one element for the v2 kernels: the plain score with
+// the scale folded into one FMA (c = scale log2 e), or with SCORED the
+// softcap / ALiBi transform of bwd_score and its derivative factor in dfac.
+template <bool SCORED>
+__device__ __forceinline__ float bwd_prob(const BwdParams& p, float raw, float c, float lse2, int row, int col,
+                                          int off, float slope_log2, float& dfac) {
+    if constexpr (SCORED) {
+        const float x = bwd_score<true>(p, raw, row, col, off, slope_log2, dfac);
+        return fast_exp2(x - lse2);
+    } else {
+        dfac = 1.0f;
+        return fast_exp2(__builtin_fmaf(raw, c, -lse2));
+    }
+}
+
 __device__ __forceinline__ bool masked_at(int row, int col, int sk, int off, int wl, int wr) {
     return (col >= sk) || (wr >= 0 && col > row + off + wr) || (wl >= 0 && col < row + off - wl);
 }
@@ -601,7 +616,7 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 
 constexpr int kLook = 3;  // operand reads in flight ahead of their MFMA (v2 kernels)
 
-template <typename T, int D, int NW, bool VARLEN, bool DROPOUT>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool SCORED = false>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {
     constexpr int BN = 64;
     constexpr int BM = 32 * NW;
@@ -675,6 +690,10 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
         dlt = p.delta[(VARLEN ? 0 : b * p.delta_b) + head * p.delta_h + sb.delta_row0 + my_row];
     }
     const float c = p.scale_log2;
+    [[maybe_unused]] float slope_log2 = 0.0f;
+    if constexpr (SCORED) {
+        if (p.alibi) slope_log2 = p.alibi[b * p.alibi_b + head] * kLog2e;
+    }
 
     f32x16 acc[DB];
 #pragma unroll
@@ -752,14 +771,15 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float pr = fast_exp2(__builtin_fmaf(s[sub][r], c, -lse2));
+                    const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    float dfac;
+                    float pr = bwd_prob<SCORED>(p, s[sub][r], c, lse2, my_row, col, off, slope_log2, dfac);
                     if (MASK == 1 || (MASK == 2 && need_mask)) {
-                        const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
                         const bool masked = (col >= sk) | (wr >= 0 & col > my_row + off + wr) |
                                             (wl >= 0 & col < my_row + off - wl);
                         pr = masked ? 0.0f : pr;
                     }
-                    dsv[r] = pr * (dp[sub][r] - dlt);
+                    dsv[r] = pr * (dp[sub][r] - dlt) * dfac;
                 }
 #pragma unroll
                 for (int t2 = 0; t2 < 2; ++t2) {
@@ -820,7 +840,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     }
 }
 
-template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool PAIRED>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool PAIRED, bool SCORED = false>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const BwdParams p) {
     // D = 128: the dK and dV accumulators (128 registers) and K (32) leave no
     // room for V in registers at 2 waves per SIMD, so V is staged once in LDS
@@ -943,6 +963,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
         const int gqa = p.gqa;
         const int ntiles = nqb * gqa;
         const float c = p.scale_log2;
+        [[maybe_unused]] float slope_log2 = 0.0f;  // per query head (tj), set per tile
 
         // Tile t is query tile nqb - 1 - t / gqa (counted from q_begin) of query
         // head kvh * gqa + t % gqa. The copies walk that order with a cursor of row
@@ -1016,6 +1037,9 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                 advance(cur);
                 copy_tile(cur, stage ^ 1);
             }
+            if constexpr (SCORED) {
+                if (p.alibi) slope_log2 = p.alibi[b * p.alibi_b + kvh * gqa + tj] * kLog2e;
+            }
 
             const bool need_mask = (key0 + BK > sk) || (wr >= 0 && key0 + BK - 1 > qb + off + wr) ||
                                    (wl >= 0 && key0 < qb + BQ - 1 + off - wl);
@@ -1072,7 +1096,13 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int r = 4 * g + e;
-                            float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                            const int prow = qb + qloc + e;
+                            float dfac;
+                            float pr = bwd_prob<SCORED>(p, s[r], c, lv[e] * kLog2e, prow, my_key, off, slope_log2, dfac);
+                            // Rows past the sequence read LSE 0 and zero Q / dO rows: a
+                            // plain score is 0 there, but an ALiBi bias alone can
+                            // overflow P (then inf x 0 in the dV MFMA).
+                            if constexpr (SCORED) pr = prow < sq ? pr : 0.0f;
                             if constexpr (MASK) {
                                 const int row = qb + qloc + e;
                                 const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
@@ -1081,7 +1111,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                             }
                             const bool kept = ((keep_bits >> r) & 1u) != 0u;
                             pv[r] = kept ? pr : 0.0f;
-                            dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
+                            dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]) * dfac;
                         }
                     }
                 };
@@ -1098,7 +1128,13 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int r = 4 * g + e;
-                            float pr = fast_exp2(__builtin_fmaf(s[r], c, -lv[e] * kLog2e));
+                            const int prow = qb + qloc + e;
+                            float dfac;
+                            float pr = bwd_prob<SCORED>(p, s[r], c, lv[e] * kLog2e, prow, my_key, off, slope_log2, dfac);
+                            // Rows past the sequence read LSE 0 and zero Q / dO rows: a
+                            // plain score is 0 there, but an ALiBi bias alone can
+                            // overflow P (then inf x 0 in the dV MFMA).
+                            if constexpr (SCORED) pr = prow < sq ? pr : 0.0f;
                             if (need_mask) {
                                 const int row = qb + qloc + e;
                                 const bool masked = (my_key >= sk) | (wr >= 0 & my_key > row + off + wr) |
@@ -1107,7 +1143,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                             }
                             const bool kept = ((keep_bits >> r) & 1u) != 0u;
                             pv[r] = kept ? pr : 0.0f;
-                            dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]);
+                            dsv[r] = pr * ((kept ? dp[r] : 0.0f) - dv4[e]) * dfac;
                         }
                     }
                 } else if (need_mask) {
@@ -1216,7 +1252,7 @@ void zero_f32(float* x, int64_t n, hipStream_t s) {
     check_launch("zero delta");
 }
 
-template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES, bool DROPOUT>
+template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES, bool DROPOUT, bool SCORED>
 void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
     if (want_kv) {
         constexpr int BK = 32 * DKV_WAVES;
@@ -1226,14 +1262,15 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
         const int64_t blocks = per_group * prm.batch * prm.kv_heads;
         if (blocks > 0) {
             const unsigned grid = static_cast<unsigned>(blocks);
-            if constexpr (!VARLEN && !DROPOUT) {
+            if constexpr (!VARLEN && !DROPOUT && !SCORED) {
                 if (prm.pair_tiles) {
                     flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, false, false, true><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
                 } else {
                     flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, false, false, false><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
                 }
             } else {
-                flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN, DROPOUT, false><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
+                flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, VARLEN, DROPOUT, false, SCORED>
+                    <<<grid, DKV_WAVES * 64, 0, s>>>(prm);
             }
             check_launch("launch flash_bwd_dkv");
         }
@@ -1243,7 +1280,8 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
         prm.blocks_per_seq = (prm.seqlen_q + BM - 1) / BM;
         const int64_t blocks = static_cast<int64_t>(prm.blocks_per_seq) * prm.batch * prm.heads;
         if (blocks > 0) {
-            flash_bwd_dq_v2_kernel<T, D, DQ_WAVES, VARLEN, DROPOUT><<<static_cast<unsigned>(blocks), DQ_WAVES * 64, 0, s>>>(prm);
+            flash_bwd_dq_v2_kernel<T, D, DQ_WAVES, VARLEN, DROPOUT, SCORED>
+                <<<static_cast<unsigned>(blocks), DQ_WAVES * 64, 0, s>>>(prm);
             check_launch("launch flash_bwd_dq");
         }
     }
@@ -1251,7 +1289,7 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
 
 template <typename T, int D, bool VARLEN, bool GEN>
 void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
-    if constexpr (!GEN && (D == 64 || D == 128)) {
+    if constexpr (D == 64 || D == 128) {
         // The tiled kernels need the full bucket width and 32-bit tile offsets.
         constexpr int64_t kMaxStride = int64_t{1} << 23;
         auto ok = [&](int64_t st) { return st >= 0 && st <= kMaxStride; };
@@ -1262,11 +1300,12 @@ void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
             // concurrent blocks then share one sequence's tiles in L2. Masked
             // dense grids keep the tile-major, longest-first order.
             prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
-            prm.pair_tiles = (prm.seq_major || prm.drop_threshold < 255) ? 0 : 1;
+            // Softcap / ALiBi (GEN): the scored instances, unpaired.
+            prm.pair_tiles = (prm.seq_major || prm.drop_threshold < 255 || GEN) ? 0 : 1;
             if (prm.drop_threshold < 255) {
-                launch_bwd_v2<T, D, VARLEN, 4, 4, true>(prm, want_q, want_kv, s);
+                launch_bwd_v2<T, D, VARLEN, 4, 4, true, GEN>(prm, want_q, want_kv, s);
             } else {
-                launch_bwd_v2<T, D, VARLEN, 4, 4, false>(prm, want_q, want_kv, s);
+                launch_bwd_v2<T, D, VARLEN, 4, 4, false, GEN>(prm, want_q, want_kv, s);
             }
             return;
         }
