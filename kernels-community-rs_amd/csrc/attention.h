@@ -76,9 +76,19 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// tanh(y) from one exp2 and one reciprocal, 1 - 2 / (e^(2|y|) + 1) with the
+// sign of y (absolute error ~1e-7; e^(2|y|) = inf gives 1). The tiled softcap
+// paths use it: libm's tanhf inlined per score is several times the VALU work
+// and registers.
+__device__ __forceinline__ float tanh_exp2(float y) {
+    const float e = fast_exp2((2.0f * kLog2e) * fabsf(y));
+    return copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), y);
+}
 constexpr float kLn2 = 0.6931471805599453f;
 
 // Launch parameters shared by the dense and varlen forward kernels. Strides are

@@ -121,15 +121,6 @@ __device__ __forceinline__ float bwd_score(const BwdParams& p, float raw, int ro
 // P = 2^(score - lse) of one element for the v2 kernels: the plain score with
 // the scale folded into one FMA (c = scale log2 e), or with SCORED the
 // softcap / ALiBi transform of bwd_score and its derivative factor in dfac.
-// tanh(y) from one exp2 and one reciprocal, 1 - 2 / (e^(2|y|) + 1) with the
-// sign of y (absolute error ~1e-7; e^(2|y|) = inf gives 1). The v2 kernels
-// use it for the softcap: libm's tanhf inlined per score costs ~50 registers
-// there.
-__device__ __forceinline__ float tanh_exp2(float y) {
-    const float e = fast_exp2((2.0f * kLog2e) * fabsf(y));
-    return copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), y);
-}
-
 template <bool SCORED>
 __device__ __forceinline__ float bwd_prob(const BwdParams& p, float raw, float c, float lse2, int row, int col,
                                           int off, float slope_log2, float& dfac) {

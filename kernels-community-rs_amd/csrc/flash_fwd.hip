@@ -673,7 +673,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
         }
 
         if constexpr (SCORED) {
-            // The general kernel's score transform (same operations, same order).
+            // The general kernel's score transform, with tanh from tanh_exp2.
             const bool cap = p.tanh_scale > 0.0f;
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
@@ -681,7 +681,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams
                 for (int r = 0; r < 16; ++r) {
                     const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
                     float x = s[sub][r];
-                    x = cap ? tanhf(x * p.tanh_scale) * p.scale_eff_log2 : x * p.scale_log2;
+                    x = cap ? tanh_exp2(x * p.tanh_scale) * p.scale_eff_log2 : x * p.scale_log2;
                     if (p.alibi) {
                         x += p.alibi_causal ? slope_log2 * static_cast<float>(col)
                                             : -slope_log2 * fabsf(static_cast<float>(row + off - col));
