@@ -215,13 +215,17 @@ def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, **kw):
     nb = len(cu_q) - 1
     dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
     delta = np.zeros((H, Tq + 128 * nb), dtype=dtype)
+    kw = dict(kw)
+    alibi = kw.pop("alibi_slopes", None)
     for b, ((qs, qe), (ks, ke)) in enumerate(zip(_slices(cu_q), _slices(cu_k))):
         if qe == qs:
             continue
+        slopes = None if alibi is None else (np.asarray(alibi)[b] if np.ndim(alibi) == 2 else alibi)
         extra = _varlen_dropout(kw, b, H, qe - qs, ke - ks)
         rest = {key: val for key, val in kw.items() if key != "dropout"}
         a, b_, c, d = backward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke], out[None, qs:qe],
-                               dout[None, qs:qe], np.asarray(lse)[None, :, qs:qe], **rest, **extra)
+                               dout[None, qs:qe], np.asarray(lse)[None, :, qs:qe], alibi_slopes=slopes,
+                               **rest, **extra)
         dq[qs:qe] = a[0]
         dk[ks:ke] += b_[0]
         dv[ks:ke] += c[0]

@@ -237,3 +237,40 @@ def test_varlen_baseline_config_backward():
               f"{np.abs(dq[a:b, hs].float().cpu().numpy() - edq[0]).max():.3g}, "
               f"|dk err| {np.abs(dk[a:b, grp].float().cpu().numpy() - edk[0, :, 0]).max():.3g}, "
               f"|dv err| {np.abs(dv[a:b, grp].float().cpu().numpy() - edv[0, :, 0]).max():.3g}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("mode", ["alibi", "softcap", "both"])
+def test_varlen_scored_forward_backward(mode, d):
+    """Packed sequences (one empty, ragged lengths) with [B, H] ALiBi slopes and / or
+    softcap: the tiled forward's and v2 backward's scored instances against the
+    oracle, at the fp16 tolerances of the dense tests."""
+    import flash_attn2_rs
+
+    g = torch.Generator().manual_seed(31 + d)
+    lens_q, lens_k = [70, 0, 129, 33], [90, 5, 129, 200]
+    cu_q = torch.tensor(np.cumsum([0] + lens_q), dtype=torch.int32)
+    cu_k = torch.tensor(np.cumsum([0] + lens_k), dtype=torch.int32)
+    h, hk = 4, 2
+    q = torch.randn(sum(lens_q), h, d, generator=g).half()
+    k = torch.randn(sum(lens_k), hk, d, generator=g).half()
+    v = torch.randn(sum(lens_k), hk, d, generator=g).half()
+    dout = torch.randn(sum(lens_q), h, d, generator=g).half()
+    slopes = (torch.rand(4, h, generator=g) * 0.2).float() if mode != "softcap" else None
+    cap = 20.0 if mode != "alibi" else 0.0
+    print(f"varlen scored mode={mode} d={d}", flush=True)
+    opts = dict(max_seqlen_q=max(lens_q), max_seqlen_k=max(lens_k), is_causal=True, softcap=cap,
+                alibi_slopes=None if slopes is None else slopes.cuda())
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out, lse, _, _ = flash_attn2_rs.varlen_fwd(qd, kd, vd, cu_q.cuda(), cu_k.cuda(), **opts)
+    dq, dk, dv, _ = flash_attn2_rs.varlen_bwd(dout.cuda(), qd, kd, vd, out, lse, cu_q.cuda(), cu_k.cuda(), **opts)
+    kw = dict(causal=True, softcap=cap, alibi_slopes=None if slopes is None else slopes.numpy())
+    eo, el = OA.varlen_forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q.numpy(),
+                               cu_k.numpy(), **kw)
+    assert np.abs(out.float().cpu().numpy() - eo).max() <= 2e-2
+    np.testing.assert_allclose(lse.cpu().numpy(), el, atol=1e-3, rtol=1e-4)
+    edq, edk, edv, _ = OA.varlen_backward(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          out.float().cpu().numpy(), dout.float().numpy(), lse.cpu().numpy(),
+                                          cu_q.numpy(), cu_k.numpy(), **kw)
+    for got, exp in ((dq, edq), (dk, edk), (dv, edv)):
+        np.testing.assert_allclose(got.float().cpu().numpy(), exp, atol=0.008, rtol=0.04)

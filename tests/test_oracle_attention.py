@@ -161,6 +161,29 @@ def test_varlen_equals_per_sequence_dense():
     assert np.all(delta[:, 17:17 + 256] == 0)
 
 
+def test_varlen_backward_per_sequence_alibi_and_softcap():
+    """[B, H] ALiBi slopes select row b for sequence b in the packed backward, as
+    in the packed forward, with softcap on top."""
+    lens_q, lens_k = [17, 0, 8], [19, 0, 12]
+    cu_q, cu_k = np.cumsum([0] + lens_q), np.cumsum([0] + lens_k)
+    q, k, v = rnd(25, 4, 16, seed=5), rnd(31, 2, 16, seed=6), rnd(31, 2, 16, seed=7)
+    slopes = np.abs(rnd(3, 4, seed=8)) * 0.1
+    kw = dict(causal=True, softcap=5.0, alibi_slopes=slopes)
+    out, lse = OA.varlen_forward(q, k, v, cu_q, cu_k, **kw)
+    dout = rnd(25, 4, 16, seed=9)
+    dq, dk, dv, _ = OA.varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, **kw)
+    for b, ((qs, qe), (ks, ke)) in enumerate(zip(zip(cu_q[:-1], cu_q[1:]), zip(cu_k[:-1], cu_k[1:]))):
+        if qe == qs:
+            continue
+        one = dict(causal=True, softcap=5.0, alibi_slopes=slopes[b])
+        o, l = OA.forward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke], **one)
+        np.testing.assert_allclose(out[qs:qe], o[0], rtol=1e-6)
+        a, bk, c, _ = OA.backward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke], o, dout[None, qs:qe], l, **one)
+        np.testing.assert_allclose(dq[qs:qe], a[0], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(dk[ks:ke], bk[0], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(dv[ks:ke], c[0], rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_probabilities_are_the_attention_matrix(causal):
     """|P| times V is torch's SDPA output (so |P| is the softmax attention matrix),
