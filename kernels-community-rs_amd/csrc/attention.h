@@ -759,6 +759,26 @@ private:
 void launch_dropout_probabilities(const FwdParams& prm, bool varlen, int dtype, void* probs, int64_t rq,
                                   int64_t rk, hipStream_t s);
 
+// A zero-padded, packed copy of an attention tensor whose last dimension is
+// widened to `width` (inputs: copied in, the extra columns zero), or a padded
+// output buffer whose first columns copy_out() writes back to the tensor.
+// Head sizes the tiled kernels do not cover run on them through these copies.
+class Padded {
+public:
+    Padded(const kcr_tensor* t, int64_t width, hipStream_t s, bool copy_in);
+    ~Padded();
+    Padded(const Padded&) = delete;
+    Padded& operator=(const Padded&) = delete;
+    const kcr_tensor* get() const { return src_ ? &padded_ : nullptr; }
+    void copy_out();
+
+private:
+    const kcr_tensor* src_;
+    kcr_tensor padded_{};
+    void* buffer_ = nullptr;
+    hipStream_t stream_;
+};
+
 // Whether two tensors' byte ranges intersect.
 bool spans_overlap(const kcr_tensor* a, const kcr_tensor* b);
 

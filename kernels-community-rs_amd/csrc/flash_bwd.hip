@@ -1522,6 +1522,24 @@ extern "C" int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
             if (dv) zero_u16(dv->data, numel(*dv), s);
             return;
         }
+        // Head sizes below 128 other than 64 run on the tiled kernels through
+        // zero-padded copies (64 or 128 wide): the zero columns add nothing to
+        // any dot product, and the gradients' first D columns are copied back.
+        const int64_t DK = D < 64 ? 64 : D < 128 ? 128 : D;
+        const bool pad = DK != D && D % 8 == 0;
+        Padded pq(pad ? q : nullptr, DK, s, true), pk(pad ? k : nullptr, DK, s, true),
+            pv(pad ? v : nullptr, DK, s, true), pdo(pad ? dout : nullptr, DK, s, true);
+        Padded pdq(pad ? dq : nullptr, DK, s, false), pdk(pad ? dk : nullptr, DK, s, false),
+            pdv(pad ? dv : nullptr, DK, s, false);
+        if (pad) {
+            q = pq.get();
+            k = pk.get();
+            v = pv.get();
+            dout = pdo.get();
+            if (dq) dq = pdq.get();
+            if (dk) dk = pdk.get();
+            if (dv) dv = pdv.get();
+        }
         BwdParams prm{};
         prm.q = q->data; prm.k = k->data; prm.v = v->data; prm.dout = dout->data;
         prm.lse = static_cast<const float*>(lse->data);
@@ -1545,11 +1563,14 @@ extern "C" int kcr_flash_bwd(const kcr_tensor* q, const kcr_tensor* k, const kcr
         prm.gqa = static_cast<int32_t>(H / Hk);
         prm.seqlen_q = static_cast<int32_t>(Sq);
         prm.seqlen_k = static_cast<int32_t>(Sk);
-        prm.head_dim = static_cast<int32_t>(D);
+        prm.head_dim = static_cast<int32_t>(pad ? DK : D);
         prm.alibi_b = alibi_b;
         fill_common(prm, opt, scale_used, drop);
-        const int bucket = static_cast<int>((D + 31) / 32 * 32);
+        const int bucket = static_cast<int>(((pad ? DK : D) + 31) / 32 * 32);
         launch_bwd<false>(prm, q->dtype, bucket, opt.tanh_scale > 0.0f || alibi, dq != nullptr, dk != nullptr, s);
+        pdq.copy_out();
+        pdk.copy_out();
+        pdv.copy_out();
     });
 }
 

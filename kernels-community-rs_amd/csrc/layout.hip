@@ -19,10 +19,11 @@ namespace {
 
 constexpr int kCopyWaves = 4;
 
-// rows = B * S * H rows of D elements. Row r = ((b * S) + s) * H + h.
+// rows = B * S * H rows: D elements copied, then the destination row zeroed
+// up to DZ elements (DZ > D for a zero-padded copy). Row r = ((b * S) + s) * H + h.
 __global__ void __launch_bounds__(64 * kCopyWaves) copy_rows_kernel(
     uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, int64_t rows, int64_t S, int64_t H,
-    int64_t D, int64_t sb, int64_t ss, int64_t sh, int64_t db, int64_t ds, int64_t dh) {
+    int64_t D, int64_t DZ, int64_t sb, int64_t ss, int64_t sh, int64_t db, int64_t ds, int64_t dh) {
     const int lane = threadIdx.x & 63;
     for (int64_t r = static_cast<int64_t>(blockIdx.x) * kCopyWaves + (threadIdx.x >> 6); r < rows;
          r += static_cast<int64_t>(gridDim.x) * kCopyWaves) {
@@ -33,6 +34,7 @@ __global__ void __launch_bounds__(64 * kCopyWaves) copy_rows_kernel(
         const uint16_t* from = src + b * sb + s * ss + h * sh;
         uint16_t* to = dst + b * db + s * ds + h * dh;
         for (int64_t c = lane; c < D; c += 64) to[c] = from[c];
+        for (int64_t c = D + lane; c < DZ; c += 64) to[c] = 0;
     }
 }
 
@@ -52,6 +54,8 @@ Dims4 dims4(const kcr_tensor& t) {
     return d;
 }
 
+// Copies the rows of `src` into `dst` (same outer shape): the first
+// min(widths) elements of each row, the rest of a wider destination row zeroed.
 void copy_rows(const kcr_tensor& dst, const kcr_tensor& src, hipStream_t s) {
     const Dims4 a = dims4(dst), b = dims4(src);
     const int64_t rows = a.shape[0] * a.shape[1] * a.shape[2];
@@ -59,7 +63,8 @@ void copy_rows(const kcr_tensor& dst, const kcr_tensor& src, hipStream_t s) {
     const int64_t blocks = std::min<int64_t>((rows + kCopyWaves - 1) / kCopyWaves, 65536);
     copy_rows_kernel<<<static_cast<unsigned>(blocks), 64 * kCopyWaves, 0, s>>>(
         static_cast<uint16_t*>(dst.data), static_cast<const uint16_t*>(src.data), rows, a.shape[1],
-        a.shape[2], a.shape[3], b.stride[0], b.stride[1], b.stride[2], a.stride[0], a.stride[1], a.stride[2]);
+        a.shape[2], std::min(a.shape[3], b.shape[3]), a.shape[3], b.stride[0], b.stride[1], b.stride[2],
+        a.stride[0], a.stride[1], a.stride[2]);
     check_launch("launch copy_rows");
 }
 
@@ -138,6 +143,34 @@ void Staged::copy_out() {
 }
 
 Staged::~Staged() {
+    if (buffer_) (void)hipFreeAsync(buffer_, stream_);
+}
+
+Padded::Padded(const kcr_tensor* t, int64_t width, hipStream_t s, bool copy_in) : src_(t), stream_(s) {
+    if (!t) return;
+    if (t->ndim < 1 || t->ndim > 4 || width < t->shape[t->ndim - 1]) {
+        throw value_error("padded attention tensors are 1-4 dimensional and only widen the last dimension");
+    }
+    padded_ = *t;
+    padded_.shape[t->ndim - 1] = width;
+    int64_t count = 1;
+    for (int i = t->ndim - 1; i >= 0; --i) {
+        padded_.strides[i] = count;
+        count *= padded_.shape[i];
+    }
+    if (count > 0) {
+        const size_t bytes = static_cast<size_t>(count) * element_size(t->dtype);
+        check_hip(hipMallocAsync(&buffer_, bytes, s), "hipMallocAsync (padded attention tensor)");
+    }
+    padded_.data = buffer_;
+    if (copy_in && buffer_) copy_rows(padded_, *t, s);
+}
+
+void Padded::copy_out() {
+    if (buffer_) copy_rows(*src_, padded_, stream_);
+}
+
+Padded::~Padded() {
     if (buffer_) (void)hipFreeAsync(buffer_, stream_);
 }
 
