@@ -1661,6 +1661,27 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
         };
         if (q->dtype == KCR_BFLOAT16) go(bf16_t{}); else go(f16_t{});
         check_launch("launch varlen preprocess");
+        // Head sizes below 128 other than 64: zero-padded copies for the tiled
+        // kernels, as in kcr_flash_bwd; the padded gradients start at zero like
+        // the caller's (rows no block writes).
+        const int64_t DK = D < 64 ? 64 : D < 128 ? 128 : D;
+        const bool pad = DK != D && D % 8 == 0;
+        Padded pq(pad ? q : nullptr, DK, s, true), pk(pad ? k : nullptr, DK, s, true),
+            pv(pad ? v : nullptr, DK, s, true), pdo(pad ? dout : nullptr, DK, s, true);
+        Padded pdq(pad ? dq : nullptr, DK, s, false), pdk(pad ? dk : nullptr, DK, s, false),
+            pdv(pad ? dv : nullptr, DK, s, false);
+        if (pad) {
+            q = pq.get();
+            k = pk.get();
+            v = pv.get();
+            dout = pdo.get();
+            dq = pdq.get();
+            dk = pdk.get();
+            dv = pdv.get();
+            zero_u16(dq->data, numel(*dq), s);
+            zero_u16(dk->data, numel(*dk), s);
+            zero_u16(dv->data, numel(*dv), s);
+        }
         BwdParams prm{};
         prm.q = q->data; prm.k = k->data; prm.v = v->data; prm.dout = dout->data;
         prm.lse = static_cast<const float*>(lse->data);
@@ -1686,10 +1707,13 @@ extern "C" int kcr_flash_varlen_bwd(const kcr_tensor* q, const kcr_tensor* k, co
         prm.gqa = static_cast<int32_t>(H / Hk);
         prm.seqlen_q = static_cast<int32_t>(max_seqlen_q);
         prm.seqlen_k = static_cast<int32_t>(max_seqlen_k);
-        prm.head_dim = static_cast<int32_t>(D);
+        prm.head_dim = static_cast<int32_t>(pad ? DK : D);
         prm.alibi_b = alibi_b;
         fill_common(prm, opt, scale_used, drop);
-        const int bucket = static_cast<int>((D + 31) / 32 * 32);
+        const int bucket = static_cast<int>(((pad ? DK : D) + 31) / 32 * 32);
         launch_bwd<true>(prm, q->dtype, bucket, opt.tanh_scale > 0.0f || alibi, true, true, s);
+        pdq.copy_out();
+        pdk.copy_out();
+        pdv.copy_out();
     });
 }

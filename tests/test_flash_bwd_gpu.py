@@ -239,12 +239,13 @@ def test_varlen_baseline_config_backward():
               f"|dv err| {np.abs(dv[a:b, grp].float().cpu().numpy() - edv[0, :, 0]).max():.3g}")
 
 
-@pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("mode", ["alibi", "softcap", "both"])
+@pytest.mark.parametrize("d", [64, 128, 48, 96])
+@pytest.mark.parametrize("mode", ["plain", "alibi", "softcap", "both"])
 def test_varlen_scored_forward_backward(mode, d):
     """Packed sequences (one empty, ragged lengths) with [B, H] ALiBi slopes and / or
     softcap: the tiled forward's and v2 backward's scored instances against the
-    oracle, at the fp16 tolerances of the dense tests."""
+    oracle, at the fp16 tolerances of the dense tests. Head sizes 48 and 96 run
+    the backward through zero-padded copies."""
     import flash_attn2_rs
 
     g = torch.Generator().manual_seed(31 + d)
@@ -256,8 +257,8 @@ def test_varlen_scored_forward_backward(mode, d):
     k = torch.randn(sum(lens_k), hk, d, generator=g).half()
     v = torch.randn(sum(lens_k), hk, d, generator=g).half()
     dout = torch.randn(sum(lens_q), h, d, generator=g).half()
-    slopes = (torch.rand(4, h, generator=g) * 0.2).float() if mode != "softcap" else None
-    cap = 20.0 if mode != "alibi" else 0.0
+    slopes = (torch.rand(4, h, generator=g) * 0.2).float() if mode in ("alibi", "both") else None
+    cap = 20.0 if mode in ("softcap", "both") else 0.0
     print(f"varlen scored mode={mode} d={d}", flush=True)
     opts = dict(max_seqlen_q=max(lens_q), max_seqlen_k=max(lens_k), is_causal=True, softcap=cap,
                 alibi_slopes=None if slopes is None else slopes.cuda())
