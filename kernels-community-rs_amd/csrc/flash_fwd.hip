@@ -1389,6 +1389,18 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
 
 int64_t round128(int64_t n) { return (n + 127) / 128 * 128; }
 
+// Head size the forward kernels run at. Head sizes below 128 that are not a
+// multiple of 32 run on the tiled kernels through zero-padded copies, 64 or
+// 128 wide (the zero columns add nothing to Q K^T, and O's first D columns are
+// copied back): the general kernel runs them at a rounded-up width with
+// per-column masks (D = 48 236 -> 326, D = 112 341 -> 490 TFLOP/s padded).
+// Multiples of 32 keep their own size: the general kernel at D = 96 (579
+// TFLOP/s) beats the padded D = 128 tiles (444).
+int64_t fwd_work_dim(int64_t D) {
+    if (D % 8 != 0 || D % 32 == 0 || D > 128) return D;
+    return D < 64 ? 64 : 128;
+}
+
 // The diagnostic-probability output of a forward with return_softmax
 // (host/forward/mod.rs:181-199, 382-398; host/varlen/mod.rs:201-209, 400-414):
 // dropout with an RNG-state tensor, and a contiguous [batch, H, ceil128(Sq),
@@ -1471,7 +1483,18 @@ void dense_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* 
         k = sk_.get();
         v = sv_.get();
         out = so_.get();
-        run_dense_fwd(q, k, v, alibi, alibi_b, opt, drop, B, Sq, H, D, Sk, Hk, out, lse, probs, s);
+        const int64_t DW = fwd_work_dim(D);
+        const bool pad = DW != D;
+        Padded pq(pad ? q : nullptr, DW, s, true), pk(pad ? k : nullptr, DW, s, true),
+            pv(pad ? v : nullptr, DW, s, true), po(pad ? out : nullptr, DW, s, false);
+        if (pad) {
+            q = pq.get();
+            k = pk.get();
+            v = pv.get();
+            out = po.get();
+        }
+        run_dense_fwd(q, k, v, alibi, alibi_b, opt, drop, B, Sq, H, DW, Sk, Hk, out, lse, probs, s);
+        po.copy_out();
         so_.copy_out();
     }
 }
@@ -1703,6 +1726,19 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
             so_.copy_out();
             return;
         }
+        // Zero-padded copies for head sizes within 3/4 of 64 or 128 (see
+        // fwd_work_dim); the padded output starts as the caller's, so rows no
+        // sequence covers come back unchanged.
+        const int64_t DW = fwd_work_dim(D);
+        const bool pad = DW != D;
+        Padded pq(pad ? q : nullptr, DW, s, true), pk(pad ? k : nullptr, DW, s, true),
+            pv(pad ? v : nullptr, DW, s, true), po(pad ? out : nullptr, DW, s, true);
+        if (pad) {
+            q = pq.get();
+            k = pk.get();
+            v = pv.get();
+            out = po.get();
+        }
         FwdParams prm{};
         prm.q = q->data;
         prm.k = k->data;
@@ -1728,7 +1764,7 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
         prm.gqa = static_cast<int32_t>(H / Hk);
         prm.seqlen_q = static_cast<int32_t>(max_seqlen_q);
         prm.seqlen_k = static_cast<int32_t>(max_seqlen_k);
-        prm.head_dim = static_cast<int32_t>(D);
+        prm.head_dim = static_cast<int32_t>(DW);
         prm.window_left = opt.window_left;
         prm.window_right = opt.window_right;
         prm.alibi_b = alibi_b;
@@ -1741,9 +1777,9 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
         // the tiles do not cover and non-positive plain scales take the general
         // kernel.
         prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
-        const bool general = D % 32 != 0 || (D != 64 && D != 128 && prm.scored) ||
+        const bool general = DW % 32 != 0 || (DW != 64 && DW != 128 && prm.scored) ||
                              (!prm.scored && !(opt.scale > 0.0f));
-        const int bucket = bucket_for(D);
+        const int bucket = bucket_for(DW);
         const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
                                    ? 1
                                    : dense_splits(batch, H, max_seqlen_q, max_seqlen_k, compute_units());
@@ -1767,6 +1803,7 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
             launch_dropout_probabilities(prm, true, q->dtype, probs->data, round128(max_seqlen_q),
                                          round128(max_seqlen_k), s);
         }
+        po.copy_out();
         so_.copy_out();
     }
 }
