@@ -1996,12 +1996,15 @@ void fwd_kvcache_impl(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_t
             prm.k_page = kcache->strides[0];
             prm.v_page = vcache->strides[0];
         }
-        // Cached attention with softcap / ALiBi stays on the general kernel.
-        const bool general = opt.tanh_scale > 0.0f || alibi != nullptr || D % 32 != 0 || !(opt.scale > 0.0f);
+        // Softcap / ALiBi run in the tiled kernels' scored instances (paged or
+        // not, with key splits); other head sizes on the general kernel.
+        prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
+        const bool general = D % 32 != 0 || (D != 64 && D != 128 && prm.scored) ||
+                             (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(D);
         const bool tiled = !general && (bucket == 64 || bucket == 128);
         if (block_table && !tiled) {
-            throw value_error("paged caches support head size 64 or 128 without softcap or ALiBi");
+            throw value_error("paged caches support head size 64 or 128 (and a positive scale)");
         }
         const int64_t splits = tiled ? std::max<int64_t>(1, num_splits) : 1;
         if (splits > 1) {

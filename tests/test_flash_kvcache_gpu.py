@@ -35,7 +35,7 @@ def _f(t):
 
 
 def _run(q, kc, vc, k, v, lengths, *, causal=False, window=(-1, -1), splits=1, cos=None, sin=None,
-         interleaved=True, idx=None, leftpad=None, table=None, softcap=0.0):
+         interleaved=True, idx=None, leftpad=None, table=None, softcap=0.0, alibi=None):
     import flash_attn2_rs
 
     dev = "cuda"
@@ -48,13 +48,14 @@ def _run(q, kc, vc, k, v, lengths, *, causal=False, window=(-1, -1), splits=1, c
         cache_leftpad=None if leftpad is None else torch.tensor(leftpad, dtype=torch.int32, device=dev),
         block_table=None if table is None else torch.tensor(table, dtype=torch.int32, device=dev),
         causal=causal, window_size=window, softcap=softcap, rotary_interleaved=interleaved,
-        num_splits=splits, return_softmax_lse=True)
+        alibi_slopes=None if alibi is None else alibi.to(dev), num_splits=splits, return_softmax_lse=True)
     torch.cuda.synchronize()
     return out.cpu(), lse.cpu(), kcd.cpu(), vcd.cpu()
 
 
 def _expect(q, kc, vc, k, v, lengths, *, causal=False, window=(-1, -1), cos=None, sin=None,
-            interleaved=True, idx=None, leftpad=None, table=None, softcap=0.0, dtype=torch.bfloat16):
+            interleaved=True, idx=None, leftpad=None, table=None, softcap=0.0, dtype=torch.bfloat16,
+            alibi=None):
     dt = DT[dtype]
     B, sq = q.shape[:2]
     snew = 0 if k is None else k.shape[1]
@@ -71,7 +72,8 @@ def _expect(q, kc, vc, k, v, lengths, *, causal=False, window=(-1, -1), cos=None
     used = np.array(lengths) + snew if lengths is not None else np.full(B, cap)
     out, lse = KV.attend(qn, kcn, vcn, used, leftpad=leftpad, cache_batch_idx=idx,
                          block_table=None if table is None else np.array(table), causal=causal,
-                         window_left=window[0], window_right=window[1], softcap=softcap)
+                         window_left=window[0], window_right=window[1], softcap=softcap,
+                         alibi_slopes=None if alibi is None else alibi.numpy())
     return out, lse, kcn, vcn
 
 
@@ -162,6 +164,27 @@ def test_readonly_full_cache_and_window():
     q, kc, vc, _, _ = _setup(B, cap, Hk, H, D, 0, 4, torch.bfloat16, seed=8)
     got = _run(q, kc, vc, None, None, None, causal=True, window=(64, 0))
     _check(got, _expect(q, kc, vc, None, None, None, causal=True, window=(64, 0)))
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("mode", ["alibi", "softcap", "both"])
+def test_scored_cache(mode, paged, splits):
+    """Softcap and / or ALiBi over a contiguous or paged cache, with key splits:
+    the tiled kernel's scored instances in cache mode, against the oracle."""
+    B, cap, Hk, H, D = 2, 512, 2, 8, 128
+    q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 3, 3, torch.bfloat16, seed=21)
+    lengths = [100, 400]
+    table = None
+    if paged:
+        # Two sequences of two 256-row pages each, pages in permuted order.
+        kc = kc.reshape(B * 2, 256, Hk, D)
+        vc = vc.reshape(B * 2, 256, Hk, D)
+        table = [[2, 0], [3, 1]]
+    alibi = (torch.rand(H, generator=torch.Generator().manual_seed(5)) * 0.2).float() if mode != "softcap" else None
+    cap_v = 30.0 if mode != "alibi" else 0.0
+    got = _run(q, kc, vc, k, v, lengths, causal=True, splits=splits, table=table, softcap=cap_v, alibi=alibi)
+    _check(got, _expect(q, kc, vc, k, v, lengths, causal=True, table=table, softcap=cap_v, alibi=alibi))
 
 
 def test_general_kernel_softcap_d96():
