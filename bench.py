@@ -142,33 +142,43 @@ def _attn_inputs(seed, b=4, hq=32, hkv=8, s=4096, d=128):
     return q, k, v
 
 
-def _wl_fa_fwd(causal, p_dropout=0.0):
+def _score_options(hq, alibi, softcap):
+    """ALiBi slopes (the usual 2^(-8 (h + 1) / H) ladder) and the softcap, for the
+    scored-kernel workloads; none by default."""
+    slopes = (2.0 ** (-8.0 * (torch.arange(hq) + 1) / hq)).float().cuda() if alibi else None
+    extra = {**({"alibi": True} if alibi else {}), **({"softcap": softcap} if softcap else {})}
+    return slopes, float(softcap), extra
+
+
+def _wl_fa_fwd(causal, p_dropout=0.0, d=128, alibi=False, softcap=0.0):
     def make():
         import flash_attn2_rs
 
-        b, hq, hkv, s, d = 4, 32, 8, 4096, 128
+        b, hq, hkv, s = 4, 32, 8, 4096
         q, k, v = _attn_inputs(3, b, hq, hkv, s, d)
         out = torch.empty_like(q)
         ops = flash_attn2_rs.ops
         drop = (p_dropout, 1234, 0) if p_dropout > 0 else ()
+        slopes, cap, extra = _score_options(hq, alibi, softcap)
 
         def run():
-            ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, *drop, out)
+            ops.fwd_lse(q, k, v, slopes, None, causal, -1, -1, cap, *drop, out)
 
         flops = 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
+        plain = not (alibi or softcap) and d == 128
         return dict(run=run, work=flops, bound="mfma", kernel="flash_fwd",
                     config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
-                            "dtype": "bf16", **({"p_dropout": p_dropout} if p_dropout else {})},
-                    cpu=lambda: cpu_attention(q, k, v, causal))
+                            "dtype": "bf16", **({"p_dropout": p_dropout} if p_dropout else {}), **extra},
+                    cpu=(lambda: cpu_attention(q, k, v, causal)) if plain else None)
 
     return make
 
 
-def _wl_fa_bwd(causal, p_dropout=0.0):
+def _wl_fa_bwd(causal, p_dropout=0.0, d=128, alibi=False, softcap=0.0):
     def make():
         import flash_attn2_rs
 
-        b, hq, hkv, s, d = 4, 32, 8, 4096, 128
+        b, hq, hkv, s = 4, 32, 8, 4096
         q, k, v = _attn_inputs(3, b, hq, hkv, s, d)
         g = _gen(4)
         dout = torch.randn(b, s, hq, d, generator=g).bfloat16().cuda()
@@ -176,8 +186,9 @@ def _wl_fa_bwd(causal, p_dropout=0.0):
         ops = flash_attn2_rs.ops
         state = torch.tensor([1234, 0], dtype=torch.int64, device="cuda") if p_dropout > 0 else None
         drop = (p_dropout, state, 0) if p_dropout > 0 else ()
-        lse = ops.fwd_lse(q, k, v, None, None, causal, -1, -1, 0.0, *drop, out)
-        args = (None, None, causal, -1, -1, 0.0, p_dropout, state)
+        slopes, cap, extra = _score_options(hq, alibi, softcap)
+        lse = ops.fwd_lse(q, k, v, slopes, None, causal, -1, -1, cap, *drop, out)
+        args = (slopes, None, causal, -1, -1, cap, p_dropout, state)
 
         def run():
             delta = ops.bwd_preprocess(dout, out, p_dropout)
@@ -186,7 +197,7 @@ def _wl_fa_bwd(causal, p_dropout=0.0):
         flops = 2.5 * 4.0 * b * hq * s * s * d * (0.5 if causal else 1.0)
         return dict(run=run, work=flops, bound="mfma", kernel="flash_bwd_dkv",
                     config={"B": b, "Hq": hq, "Hkv": hkv, "S": s, "D": d, "causal": causal,
-                            "dtype": "bf16", **({"p_dropout": p_dropout} if p_dropout else {})},
+                            "dtype": "bf16", **({"p_dropout": p_dropout} if p_dropout else {}), **extra},
                     cpu=None)
 
     return make
@@ -374,6 +385,14 @@ WORKLOADS = {
     "fa_bwd": _wl_fa_bwd(False),
     "fa_fwd_causal_dropout": _wl_fa_fwd(True, 0.1),
     "fa_bwd_causal_dropout": _wl_fa_bwd(True, 0.1),
+    # Opt-in (not in the default run): the scored (ALiBi / softcap) and padded
+    # (head sizes 96 / 112) attention paths at the BASELINE shape.
+    "fa_fwd_causal_alibi": _wl_fa_fwd(True, alibi=True),
+    "fa_fwd_causal_softcap": _wl_fa_fwd(True, softcap=30.0),
+    "fa_bwd_causal_alibi": _wl_fa_bwd(True, alibi=True),
+    "fa_bwd_causal_softcap": _wl_fa_bwd(True, softcap=30.0),
+    "fa_fwd_causal_d112": _wl_fa_fwd(True, d=112),
+    "fa_bwd_causal_d96": _wl_fa_bwd(True, d=96),
     "fa_varlen_fwd": _wl_fa_varlen("fwd"),
     "fa_varlen_bwd": _wl_fa_varlen("bwd"),
     "rms_norm": wl_rmsnorm,
@@ -390,7 +409,9 @@ WORKLOADS = {
     "hbm_copy": wl_hbm_copy,
     "gemm_ceiling": wl_gemm_ceiling,
 }
-DEFAULT_ORDER = [n for n in WORKLOADS if n not in ("hbm_copy", "gemm_ceiling")]
+OPT_IN = ("hbm_copy", "gemm_ceiling", "fa_fwd_causal_alibi", "fa_fwd_causal_softcap", "fa_bwd_causal_alibi",
+          "fa_bwd_causal_softcap", "fa_fwd_causal_d112", "fa_bwd_causal_d96")
+DEFAULT_ORDER = [n for n in WORKLOADS if n not in OPT_IN]
 # Ops whose CPU baseline is timed in every default run (bounded samples).
 CPU_OPS = ("fa_fwd_causal", "fa_fwd_config1", "rms_norm", "silu_and_mul")
 
