@@ -119,22 +119,23 @@ __device__ __forceinline__ float bwd_score(const BwdParams& p, float raw, int ro
 }
 
 // P = 2^(score - lse) of one element for the v2 kernels: the plain score with
-// the scale folded into one FMA (c = scale log2 e), or with SCORED the
-// softcap / ALiBi transform of bwd_score and its derivative factor in dfac.
-template <bool SCORED>
+// the scale folded into one FMA (c = scale log2 e) for SCORED = 0; the ALiBi
+// bias added for SCORED = 1; the softcap (and any ALiBi bias) with its
+// derivative factor in dfac for SCORED = 2.
+template <int SCORED>
 __device__ __forceinline__ float bwd_prob(const BwdParams& p, float raw, float c, float lse2, int row, int col,
                                           int off, float slope_log2, float& dfac) {
-    if constexpr (SCORED) {
+    if constexpr (SCORED != 0) {
         float x;
         dfac = 1.0f;
-        if (p.tanh_scale > 0.0f) {
+        if constexpr (SCORED == 2) {
             const float t = tanh_exp2(raw * p.tanh_scale);
             dfac = 1.0f - t * t;
             x = t * p.scale_eff_log2;
         } else {
             x = raw * p.scale_log2;
         }
-        if (p.alibi) {
+        if (SCORED == 1 || p.alibi) {
             x += p.alibi_causal ? slope_log2 * static_cast<float>(col)
                                 : -slope_log2 * fabsf(static_cast<float>(row + off - col));
         }
@@ -628,7 +629,7 @@ __global__ void __launch_bounds__(NW * 64) flash_bwd_dq_kernel(const BwdParams p
 
 constexpr int kLook = 3;  // operand reads in flight ahead of their MFMA (v2 kernels)
 
-template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool SCORED = false>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, int SCORED = 0>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const BwdParams p) {
     constexpr int BN = 64;
     constexpr int BM = 32 * NW;
@@ -769,8 +770,8 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
         u32x4 pk[4];
         // The mask test is hoisted out of the element loop: one branch per
         // tile instead of a scalar branch per element.
-        // MASK: 0 none, 1 masked, 2 tested per element (the dropout kernels,
-        // where two copies of the loop would spill).
+        // MASK: 0 none, 1 masked, 2 tested per element (the dropout and scored
+        // kernels, where two copies of the loop would spill).
         auto ds_tile = [&](auto mask_tag) __attribute__((always_inline)) {
             constexpr int MASK = decltype(mask_tag)::value;
 #pragma unroll
@@ -802,7 +803,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
                 }
             }
         };
-        if constexpr (DROPOUT) {
+        if constexpr (DROPOUT || SCORED != 0) {
             ds_tile(std::integral_constant<int, 2>{});
         } else if (need_mask) {
             ds_tile(std::integral_constant<int, 1>{});
@@ -852,7 +853,7 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dq_v2_kernel(const 
     }
 }
 
-template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool PAIRED, bool SCORED = false>
+template <typename T, int D, int NW, bool VARLEN, bool DROPOUT, bool PAIRED, int SCORED = 0>
 __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const BwdParams p) {
     // D = 128: the dK and dV accumulators (128 registers) and K (32) leave no
     // room for V in registers at 2 waves per SIMD, so V is staged once in LDS
@@ -1127,9 +1128,9 @@ __global__ void __launch_bounds__(NW * 64, 8 / NW) flash_bwd_dkv_v2_kernel(const
                         }
                     }
                 };
-                if constexpr (DROPOUT) {
-                    // The dropout kernel keeps the per-element test inline: through
-                    // the lambda it spills.
+                if constexpr (DROPOUT || SCORED != 0) {
+                    // The dropout and scored kernels keep the per-element test
+                    // inline: two inlined copies of the loop spill.
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int qloc = 32 * qc + 8 * g + 4 * hh;
@@ -1264,7 +1265,7 @@ void zero_f32(float* x, int64_t n, hipStream_t s) {
     check_launch("zero delta");
 }
 
-template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES, bool DROPOUT, bool SCORED>
+template <typename T, int D, bool VARLEN, int DKV_WAVES, int DQ_WAVES, bool DROPOUT, int SCORED>
 void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
     if (want_kv) {
         constexpr int BK = 32 * DKV_WAVES;
@@ -1274,7 +1275,7 @@ void launch_bwd_v2(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
         const int64_t blocks = per_group * prm.batch * prm.kv_heads;
         if (blocks > 0) {
             const unsigned grid = static_cast<unsigned>(blocks);
-            if constexpr (!VARLEN && !DROPOUT && !SCORED) {
+            if constexpr (!VARLEN && !DROPOUT && SCORED == 0) {
                 if (prm.pair_tiles) {
                     flash_bwd_dkv_v2_kernel<T, D, DKV_WAVES, false, false, true><<<grid, DKV_WAVES * 64, 0, s>>>(prm);
                 } else {
@@ -1312,12 +1313,25 @@ void launch_bwd_t(BwdParams prm, bool want_q, bool want_kv, hipStream_t s) {
             // concurrent blocks then share one sequence's tiles in L2. Masked
             // dense grids keep the tile-major, longest-first order.
             prm.seq_major = (VARLEN || (prm.window_left < 0 && prm.window_right < 0)) ? 1 : 0;
-            // Softcap / ALiBi (GEN): the scored instances, unpaired.
+            // Softcap / ALiBi (GEN): the scored instances (1: ALiBi only, 2:
+            // softcap with or without ALiBi), unpaired.
             prm.pair_tiles = (prm.seq_major || prm.drop_threshold < 255 || GEN) ? 0 : 1;
-            if (prm.drop_threshold < 255) {
-                launch_bwd_v2<T, D, VARLEN, 4, 4, true, GEN>(prm, want_q, want_kv, s);
+            auto go = [&](auto mode_tag) {
+                constexpr int MODE = decltype(mode_tag)::value;
+                if (prm.drop_threshold < 255) {
+                    launch_bwd_v2<T, D, VARLEN, 4, 4, true, MODE>(prm, want_q, want_kv, s);
+                } else {
+                    launch_bwd_v2<T, D, VARLEN, 4, 4, false, MODE>(prm, want_q, want_kv, s);
+                }
+            };
+            if constexpr (GEN) {
+                if (prm.tanh_scale > 0.0f) {
+                    go(std::integral_constant<int, 2>{});
+                } else {
+                    go(std::integral_constant<int, 1>{});
+                }
             } else {
-                launch_bwd_v2<T, D, VARLEN, 4, 4, false, GEN>(prm, want_q, want_kv, s);
+                go(std::integral_constant<int, 0>{});
             }
             return;
         }
