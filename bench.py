@@ -393,6 +393,8 @@ WORKLOADS = {
     "fa_bwd_causal_softcap": _wl_fa_bwd(True, softcap=30.0),
     "fa_fwd_causal_d112": _wl_fa_fwd(True, d=112),
     "fa_bwd_causal_d96": _wl_fa_bwd(True, d=96),
+    "fa_fwd_causal_d256": _wl_fa_fwd(True, d=256),
+    "fa_bwd_causal_d256": _wl_fa_bwd(True, d=256),
     "fa_varlen_fwd": _wl_fa_varlen("fwd"),
     "fa_varlen_bwd": _wl_fa_varlen("bwd"),
     "rms_norm": wl_rmsnorm,
@@ -410,7 +412,8 @@ WORKLOADS = {
     "gemm_ceiling": wl_gemm_ceiling,
 }
 OPT_IN = ("hbm_copy", "gemm_ceiling", "fa_fwd_causal_alibi", "fa_fwd_causal_softcap", "fa_bwd_causal_alibi",
-          "fa_bwd_causal_softcap", "fa_fwd_causal_d112", "fa_bwd_causal_d96")
+          "fa_bwd_causal_softcap", "fa_fwd_causal_d112", "fa_bwd_causal_d96",
+          "fa_fwd_causal_d256", "fa_bwd_causal_d256")
 DEFAULT_ORDER = [n for n in WORKLOADS if n not in OPT_IN]
 # Ops whose CPU baseline is timed in every default run (bounded samples).
 CPU_OPS = ("fa_fwd_causal", "fa_fwd_config1", "rms_norm", "silu_and_mul")

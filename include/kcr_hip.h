@@ -225,7 +225,7 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
  *   rows [leftpad_k[b], seqused_k[b] + new_keys) (seqused_k: cache lengths before
  *   an append of new_keys rows; NULL: every row of the cache, new_keys ignored)
  *   of cache batch cache_batch_idx[b] (or b), or of pages block_table[b, :]
- *   (int32 [B, max_blocks]; head size 64 or 128, no softcap/ALiBi). out like q;
+ *   (int32 [B, max_blocks]; head size 64, 128 or 256). out like q;
  *   lse float32 [H, Tq]. Batched form: cu_seqlens_q NULL, q and out [B, R, H, D]
  *   with any 16-byte aligned row strides (e.g. the grouped decode view of
  *   [B, 1, H*G, D] as [B, G, H, D]) and lse float32 [B, H, R] with unit last
@@ -233,8 +233,8 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
  *   capacity.
  *   num_splits > 1 splits each query tile's keys over that many blocks; the fp32
  *   partials go to `workspace` (kcr_flash_fwd_kvcache_workspace_bytes bytes,
- *   16-byte aligned) and a merge kernel writes out/lse. Softcap / ALiBi / other
- *   head sizes run unsplit. */
+ *   16-byte aligned) and a merge kernel writes out/lse. Head sizes other than 64
+ *   and 128 run unsplit. */
 int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int64_t heads, int64_t total_q,
                                               int64_t head_dim);
 int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,

@@ -323,20 +323,22 @@ inline bool rows_aligned16(const kcr_tensor* t) {
     return true;
 }
 
-// XOR swizzle of the 16-byte chunks of a row-major LDS tile row with CH = 16
-// (D = 128, 256-byte rows) or CH = 8 (D = 64, 128-byte rows): the chunk of
-// row r is stored at chunk ^ kv_swizzle(r). Chosen for gfx950's 256-byte LDS
+// XOR swizzle of the 16-byte chunks of a row-major LDS tile row with CH = 32
+// (D = 256, 512-byte rows), CH = 16 (D = 128, 256-byte rows) or CH = 8 (D = 64,
+// 128-byte rows): the chunk of row r is stored at chunk ^ kv_swizzle(r). Chosen for gfx950's 256-byte LDS
 // bank window (measured on the device):
 //   - ds_read_b128 serves 16 lanes per pass; they read 16 consecutive rows at one
 //     logical chunk, and the swizzle maps those rows to 16 distinct 16-byte slots;
 //   - ds_read_b64_tr_b16 serves 32 lanes per pass; they read 4 rows x 4 chunks,
 //     and the swizzle gives each of the 4 rows its own 64-byte quarter.
 // The value depends on row bits 0..3 only, so row offsets that are multiples of
-// 16 keep it.
+// 16 keep it. A 512-byte row spans the bank window twice, so every row starts
+// at bank 0 as with CH = 16; the CH = 16 values (< 16) then place the chunks
+// in the same banks, and leave chunk bit 4 (which half of the row) unchanged.
 template <int CH>
 __device__ __forceinline__ int kv_swizzle(int row) {
-    static_assert(CH == 8 || CH == 16, "16-byte chunks per row: 8 or 16");
-    if constexpr (CH == 16) {
+    static_assert(CH == 8 || CH == 16 || CH == 32, "16-byte chunks per row: 8, 16 or 32");
+    if constexpr (CH >= 16) {
         return 4 * (row & 3) + ((row >> 2) & 3);
     } else {
         return 4 * ((row >> 1) & 1) + ((row >> 2) & 1);

@@ -25,9 +25,9 @@
 //     one KV head are placed on one XCD (blocks are dealt round-robin over the 8
 //     XCDs) so their K/V tiles hit the same L2.
 //
-// flash_fwd_tiled_kernel (plain scaled dot product, head size 64 or 128) copies
-// K/V tiles HBM -> LDS with direct buffer loads into swizzled row-major tiles;
-// flash_fwd_kernel (softcap, ALiBi, other head sizes, non-positive scales)
+// flash_fwd_tiled_kernel (head sizes 64, 128 and 256, plain or with softcap /
+// ALiBi) copies K/V tiles HBM -> LDS with direct buffer loads into swizzled
+// row-major tiles; flash_fwd_kernel (other head sizes, non-positive scales)
 // stages the tiles through registers and stores V transposed.
 
 #include "attention.h"
@@ -441,14 +441,15 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 }
 
 // ---------------------------------------------------------------------------
-// Tiled forward (plain scaled dot product, head size 64 or 128). One block =
+// Tiled forward (head size 64, 128 or 256). One block =
 // 4 waves = 128 query rows of one head; each wave owns 32 rows, their Q in
 // registers as the B operand of S^T = K Q^T (one query per lane: the row max and
 // sum are in-lane reductions plus one cross-half shuffle). K and V tiles of 64
 // keys are copied HBM -> LDS by direct buffer loads into row-major tiles with
 // XOR-swizzled 16-byte chunks (no staging registers, no VALU); K is read with
 // ds_read_b128 and V^T, the A operand of O^T = V^T P^T, with ds_read_b64_tr_b16
-// from the same row-major tile. P^T stays in registers: the fp32 scores are
+// from the same row-major tile (D = 256: 128 KB of tiles and 512 registers per
+// lane, one block per CU). P^T stays in registers: the fp32 scores are
 // packed in place into the B operand of the PV MFMA. Two LDS stages, the next
 // tile's copy in flight during the current tile, one barrier per tile. STREAM:
 // every K/V tile is read by this block only (cache decode with grouped rows),
@@ -457,7 +458,7 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // then runs with the scale already applied.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool VARLEN, bool DROPOUT, bool STREAM, bool SCORED = false>
-__global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(const FwdParams p) {
     constexpr int NW = 4;
     constexpr int BN = kBN;
     constexpr int BM = 32 * NW;
@@ -1296,7 +1297,7 @@ void launch_pp(FwdParams& prm, hipStream_t s) {
 
 template <typename T, int D, bool VARLEN>
 void launch_d(FwdParams& prm, bool general, hipStream_t s) {
-    if constexpr (D == 64 || D == 128) {
+    if constexpr (D == 64 || D == 128 || D == 256) {
         if (!general) {
             // Dense unmasked D = 128 without dropout: the ping-pong kernel
             // (measured faster there; the 128-row tiled kernel wins on causal,
@@ -1607,7 +1608,7 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
         // the tiles do not cover and non-positive plain scales take the general
         // kernel.
         prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
-        const bool general = D % 32 != 0 || (D != 64 && D != 128 && prm.scored) ||
+        const bool general = D % 32 != 0 || (D != 64 && D != 128 && D != 256 && prm.scored) ||
                              (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(D);
         const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
@@ -1777,7 +1778,7 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
         // the tiles do not cover and non-positive plain scales take the general
         // kernel.
         prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
-        const bool general = DW % 32 != 0 || (DW != 64 && DW != 128 && prm.scored) ||
+        const bool general = DW % 32 != 0 || (DW != 64 && DW != 128 && DW != 256 && prm.scored) ||
                              (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(DW);
         const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
@@ -1999,14 +2000,15 @@ void fwd_kvcache_impl(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_t
         // Softcap / ALiBi run in the tiled kernels' scored instances (paged or
         // not, with key splits); other head sizes on the general kernel.
         prm.scored = (opt.tanh_scale > 0.0f || alibi != nullptr) ? 1 : 0;
-        const bool general = D % 32 != 0 || (D != 64 && D != 128 && prm.scored) ||
+        const bool general = D % 32 != 0 || (D != 64 && D != 128 && D != 256 && prm.scored) ||
                              (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(D);
-        const bool tiled = !general && (bucket == 64 || bucket == 128);
+        const bool tiled = !general && (bucket == 64 || bucket == 128 || bucket == 256);
         if (block_table && !tiled) {
-            throw value_error("paged caches support head size 64 or 128 (and a positive scale)");
+            throw value_error("paged caches support head size 64, 128 or 256 (and a positive scale)");
         }
-        const int64_t splits = tiled ? std::max<int64_t>(1, num_splits) : 1;
+        // The split merge covers up to 128 columns; D = 256 runs unsplit.
+        const int64_t splits = (tiled && bucket <= 128) ? std::max<int64_t>(1, num_splits) : 1;
         if (splits > 1) {
             const int64_t need = kcr_flash_fwd_kvcache_workspace_bytes(splits, H, Tq, D);
             if (noalloc && need > workspace_bytes) {

@@ -43,6 +43,8 @@ PARITY_CASES = [
     *[case(f"d{d}-causal-gqa", 2, 8, 2, 256, 256, causal=True, head_dim=d) for d in (32, 64, 96, 256)],
     *[case(f"d{d}-causal-mha", 2, 4, 4, 256, 256, causal=True, head_dim=d) for d in (8, 48, 72, 160, 200, 224)],
     case("d64-softcap-causal", 1, 4, 4, 192, 192, causal=True, softcap=30.0, head_dim=64),
+    case("d256-softcap-alibi-gqa-causal", 2, 8, 2, 256, 256, causal=True, softcap=20.0, alibi=True, head_dim=256),
+    case("d256-window-odd-s300", 1, 4, 4, 300, 300, window_left=64, window_right=16, head_dim=256),
     case("bf16-full-mha", 2, 4, 4, 256, 256, dtype=torch.bfloat16),
     case("bf16-causal-gqa", 2, 8, 2, 256, 256, causal=True, dtype=torch.bfloat16),
     case("bf16-softcap-causal", 2, 4, 4, 256, 256, causal=True, softcap=30.0, dtype=torch.bfloat16),

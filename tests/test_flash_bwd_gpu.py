@@ -239,13 +239,14 @@ def test_varlen_baseline_config_backward():
               f"|dv err| {np.abs(dv[a:b, grp].float().cpu().numpy() - edv[0, :, 0]).max():.3g}")
 
 
-@pytest.mark.parametrize("d", [64, 128, 48, 96])
+@pytest.mark.parametrize("d", [64, 128, 48, 96, 192, 256])
 @pytest.mark.parametrize("mode", ["plain", "alibi", "softcap", "both"])
 def test_varlen_scored_forward_backward(mode, d):
     """Packed sequences (one empty, ragged lengths) with [B, H] ALiBi slopes and / or
     softcap: the tiled forward's and v2 backward's scored instances against the
     oracle, at the fp16 tolerances of the dense tests. Head sizes 48 and 96 run
-    the backward through zero-padded copies."""
+    the backward through zero-padded copies; 192 and 256 the general kernels'
+    separate dV and dK passes."""
     import flash_attn2_rs
 
     g = torch.Generator().manual_seed(31 + d)

@@ -72,7 +72,7 @@ def test_forward_mask_readout_varlen():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal,d,alibi", [(True, 128, False), (False, 64, False), (True, 96, False),
-                                            (True, 128, True)])
+                                            (True, 128, True), (True, 256, False), (False, 192, True)])
 def test_forward_backward_parity_dense(dtype, causal, d, alibi):
     import flash_attn2_rs
 

@@ -187,6 +187,26 @@ def test_scored_cache(mode, paged, splits):
     _check(got, _expect(q, kc, vc, k, v, lengths, causal=True, table=table, softcap=cap_v, alibi=alibi))
 
 
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("mode", ["plain", "both"])
+def test_cache_d256(mode, paged):
+    """Head size 256 over a contiguous or paged cache, plain or with softcap and
+    ALiBi: the tiled kernel's D = 256 instances in cache mode (a split request
+    runs unsplit)."""
+    B, cap, Hk, H, D = 2, 512, 2, 4, 256
+    q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 3, 3, torch.bfloat16, seed=23)
+    lengths = [130, 400]
+    table = None
+    if paged:
+        kc = kc.reshape(B * 2, 256, Hk, D)
+        vc = vc.reshape(B * 2, 256, Hk, D)
+        table = [[3, 1], [0, 2]]
+    alibi = (torch.rand(H, generator=torch.Generator().manual_seed(6)) * 0.2).float() if mode == "both" else None
+    cap_v = 30.0 if mode == "both" else 0.0
+    got = _run(q, kc, vc, k, v, lengths, causal=True, splits=3, table=table, softcap=cap_v, alibi=alibi)
+    _check(got, _expect(q, kc, vc, k, v, lengths, causal=True, table=table, softcap=cap_v, alibi=alibi))
+
+
 def test_general_kernel_softcap_d96():
     B, cap, Hk, H, D = 2, 300, 1, 2, 96
     q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 2, 2, torch.bfloat16, seed=9)
