@@ -1396,8 +1396,11 @@ int64_t round128(int64_t n) { return (n + 127) / 128 * 128; }
 // copied back): the general kernel runs them at a rounded-up width with
 // per-column masks (D = 48 236 -> 326, D = 112 341 -> 490 TFLOP/s padded).
 // Multiples of 32 keep their own size: the general kernel at D = 96 (579
-// TFLOP/s) beats the padded D = 128 tiles (444).
+// TFLOP/s) beats the padded D = 128 tiles (444). Above 192 the D = 256 tiles
+// (~740 TFLOP/s at 256) beat the general kernel (~475 at D = 224) with the
+// padding's extra work and copies; at 192 and below they do not.
 int64_t fwd_work_dim(int64_t D) {
+    if (D > 192 && D < 256 && D % 8 == 0) return 256;
     if (D % 8 != 0 || D % 32 == 0 || D > 128) return D;
     return D < 64 ? 64 : 128;
 }
