@@ -233,8 +233,8 @@ int kcr_flash_cache_update(const kcr_tensor* q, const kcr_tensor* kcache, const 
  *   capacity.
  *   num_splits > 1 splits each query tile's keys over that many blocks; the fp32
  *   partials go to `workspace` (kcr_flash_fwd_kvcache_workspace_bytes bytes,
- *   16-byte aligned) and a merge kernel writes out/lse. Head sizes other than 64
- *   and 128 run unsplit. */
+ *   16-byte aligned) and a merge kernel writes out/lse. Head sizes other than 64,
+ *   128 and 256 run unsplit. */
 int64_t kcr_flash_fwd_kvcache_workspace_bytes(int64_t num_splits, int64_t heads, int64_t total_q,
                                               int64_t head_dim);
 int kcr_flash_fwd_kvcache(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_tensor* vcache,

@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace kcr {
@@ -1108,7 +1109,8 @@ __global__ void __launch_bounds__(512, 1) flash_fwd_pp_kernel(const FwdParams p)
 // Split-KV merge (flash-attn2-rs/src/device/varlen/merge.rs): per row,
 // LSE = log sum_i exp(LSE_i) and O = sum_i exp(LSE_i - LSE) O_i over the splits;
 // a row no split saw gets O = 0 and LSE = +inf, as an empty row does. One wave
-// per (head, packed row); lane l < D / 2 owns columns 2l and 2l + 1. Packed row
+// per (head, packed row); lane l < D / PER owns columns PER l .. PER l + PER - 1
+// (PER = 2, or 4 at D = 256). Packed row
 // t is row t % rows_per_seq of sequence t / rows_per_seq in out / lse
 // (rows_per_seq = total_q with zero batch strides for packed outputs).
 constexpr uint32_t kUnseenLse = 0x7FC0DEADu;  // a quiet-NaN payload no kernel computes
@@ -1120,8 +1122,9 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restri
                                                            uint16_t* __restrict__ o, int64_t o_b, int64_t o_s,
                                                            int64_t o_h, float* __restrict__ lse, int64_t lse_b,
                                                            int64_t lse_h) {
-    static_assert(D % 2 == 0 && D <= 128, "two columns per lane");
-    constexpr int PER = 2;
+    constexpr int PER = D > 128 ? 4 : 2;
+    static_assert(D % PER == 0 && D / PER <= 64, "one wave covers the row");
+    using Vec = std::conditional_t<PER == 4, float4, float2>;
     const int lane = threadIdx.x & 63;
     const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (item >= static_cast<int64_t>(heads) * total_q) return;
@@ -1148,10 +1151,10 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restri
         for (int sh = 32; sh > 0; sh >>= 1) sum += __shfl_xor(sum, sh, 64);
         out_lse = mx + logf(sum);
         const float w0 = expf(l0 - out_lse), w1 = expf(l1 - out_lse);
-        const int col = PER * (lane < D / 2 ? lane : 0);
+        const int col = PER * (lane < D / PER ? lane : 0);
         for (int i0 = 0; i0 < n_splits; i0 += 8) {
             float w[8];
-            float2 v[8];
+            Vec v[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int i = i0 + u;
@@ -1159,24 +1162,32 @@ __global__ void __launch_bounds__(256) merge_splits_kernel(const float* __restri
                 // A split that saw no key of the row has weight 0 and may hold
                 // no partial row at all: its values are never used.
                 v[u] = (i < n_splits && w[u] != 0.0f)
-                           ? *reinterpret_cast<const float2*>(o_part + (i * stride + item) * D + col)
-                           : float2{0.0f, 0.0f};
+                           ? *reinterpret_cast<const Vec*>(o_part + (i * stride + item) * D + col)
+                           : Vec{};
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 if (i0 + u < n_splits && w[u] != 0.0f) {
                     acc[0] += w[u] * v[u].x;
                     acc[1] += w[u] * v[u].y;
+                    if constexpr (PER == 4) {
+                        acc[2] += w[u] * v[u].z;
+                        acc[3] += w[u] * v[u].w;
+                    }
                 }
             }
         }
     }
     const int seq = row / rows_per_seq;
     const int r = row - seq * rows_per_seq;
-    if (lane < D / 2) {
+    if (lane < D / PER) {
         uint16_t* dst =
             o + seq * o_b + static_cast<int64_t>(r) * o_s + static_cast<int64_t>(head) * o_h + PER * lane;
-        *reinterpret_cast<uint32_t*>(dst) = pack2<T>(acc[0], acc[1]);
+        if constexpr (PER == 4) {
+            *reinterpret_cast<uint2*>(dst) = uint2{pack2<T>(acc[0], acc[1]), pack2<T>(acc[2], acc[3])};
+        } else {
+            *reinterpret_cast<uint32_t*>(dst) = pack2<T>(acc[0], acc[1]);
+        }
     }
     if (lane == 0) lse[seq * lse_b + static_cast<int64_t>(head) * lse_h + r] = out_lse;
 }
@@ -1538,6 +1549,10 @@ void launch_merge(const FwdParams& prm, int dtype, int bucket, int rows, hipStre
             merge_splits_kernel<T, 64><<<grid, 256, 0, s>>>(
                 prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
                 static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
+        } else if (bucket == 256) {
+            merge_splits_kernel<T, 256><<<grid, 256, 0, s>>>(
+                prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
+                static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
         } else {
             merge_splits_kernel<T, 128><<<grid, 256, 0, s>>>(
                 prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
@@ -1553,7 +1568,8 @@ void launch_merge(const FwdParams& prm, int dtype, int bucket, int rows, hipStre
 }
 
 // Key splits for a dense call whose query tiles cannot fill the chip: enough
-// splits for about two blocks per CU (the tiled kernel runs two per CU), each
+// splits for about two blocks per CU (the tiled kernel runs two per CU, one at
+// D = 256), each
 // split at least 256 keys, at most 32 (the reference's bounds,
 // host/forward/dispatch.rs:166-181). 1 means no split.
 int64_t dense_splits(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int cus) {
@@ -1614,7 +1630,7 @@ void run_dense_fwd(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor* v
         const bool general = D % 32 != 0 || (D != 64 && D != 128 && D != 256 && prm.scored) ||
                              (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(D);
-        const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
+        const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128 && bucket != 256) || prm.drop_threshold < 255)
                                    ? 1
                                    : dense_splits(B, H, Sq, Sk, compute_units());
         // The probabilities read the final LSE (after any merge).
@@ -1784,7 +1800,7 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
         const bool general = DW % 32 != 0 || (DW != 64 && DW != 128 && DW != 256 && prm.scored) ||
                              (!prm.scored && !(opt.scale > 0.0f));
         const int bucket = bucket_for(DW);
-        const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128) || prm.drop_threshold < 255)
+        const int64_t splits = (general || prm.scored || (bucket != 64 && bucket != 128 && bucket != 256) || prm.drop_threshold < 255)
                                    ? 1
                                    : dense_splits(batch, H, max_seqlen_q, max_seqlen_k, compute_units());
         if (splits <= 1) {
@@ -2010,8 +2026,7 @@ void fwd_kvcache_impl(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_t
         if (block_table && !tiled) {
             throw value_error("paged caches support head size 64, 128 or 256 (and a positive scale)");
         }
-        // The split merge covers up to 128 columns; D = 256 runs unsplit.
-        const int64_t splits = (tiled && bucket <= 128) ? std::max<int64_t>(1, num_splits) : 1;
+        const int64_t splits = tiled ? std::max<int64_t>(1, num_splits) : 1;
         if (splits > 1) {
             const int64_t need = kcr_flash_fwd_kvcache_workspace_bytes(splits, H, Tq, D);
             if (noalloc && need > workspace_bytes) {
@@ -2041,6 +2056,10 @@ void fwd_kvcache_impl(const kcr_tensor* q, const kcr_tensor* kcache, const kcr_t
                 using T = decltype(tag);
                 if (bucket == 64) {
                     merge_splits_kernel<T, 64><<<grid, 256, 0, s>>>(
+                        prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
+                        static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
+                } else if (bucket == 256) {
+                    merge_splits_kernel<T, 256><<<grid, 256, 0, s>>>(
                         prm.o_part, prm.lse_part, prm.n_splits, prm.heads, prm.total_q, rows,
                         static_cast<uint16_t*>(prm.o), prm.o_b, prm.o_s, prm.o_h, prm.lse, prm.lse_b, prm.lse_h);
                 } else {

@@ -191,8 +191,8 @@ def test_scored_cache(mode, paged, splits):
 @pytest.mark.parametrize("mode", ["plain", "both"])
 def test_cache_d256(mode, paged):
     """Head size 256 over a contiguous or paged cache, plain or with softcap and
-    ALiBi: the tiled kernel's D = 256 instances in cache mode (a split request
-    runs unsplit)."""
+    ALiBi, with key splits: the tiled kernel's D = 256 instances in cache mode
+    and the 4-column merge."""
     B, cap, Hk, H, D = 2, 512, 2, 4, 256
     q, kc, vc, k, v = _setup(B, cap, Hk, H, D, 3, 3, torch.bfloat16, seed=23)
     lengths = [130, 400]
