@@ -446,11 +446,11 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // 4 waves = 128 query rows of one head; each wave owns 32 rows, their Q in
 // registers as the B operand of S^T = K Q^T (one query per lane: the row max and
 // sum are in-lane reductions plus one cross-half shuffle). K and V tiles of 64
-// keys are copied HBM -> LDS by direct buffer loads into row-major tiles with
+// keys (32 at D = 256) are copied HBM -> LDS by direct buffer loads into row-major tiles with
 // XOR-swizzled 16-byte chunks (no staging registers, no VALU); K is read with
 // ds_read_b128 and V^T, the A operand of O^T = V^T P^T, with ds_read_b64_tr_b16
-// from the same row-major tile (D = 256: 128 KB of tiles and 512 registers per
-// lane, one block per CU). P^T stays in registers: the fp32 scores are
+// from the same row-major tile. Two blocks per CU at every head size. P^T stays
+// in registers: the fp32 scores are
 // packed in place into the B operand of the PV MFMA. Two LDS stages, the next
 // tile's copy in flight during the current tile, one barrier per tile. STREAM:
 // every K/V tile is read by this block only (cache decode with grouped rows),
@@ -459,9 +459,12 @@ __global__ void __launch_bounds__(NW * 64, QT == 1 ? 2 : 1) flash_fwd_kernel(con
 // then runs with the scale already applied.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool VARLEN, bool DROPOUT, bool STREAM, bool SCORED = false>
-__global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(256, 2) flash_fwd_tiled_kernel(const FwdParams p) {
     constexpr int NW = 4;
-    constexpr int BN = kBN;
+    // D = 256 takes 32-key tiles: O (128), Q (64) and S (16) registers then fit
+    // two waves per SIMD, and 64 KB of tiles two blocks per CU.
+    constexpr int BN = D > 128 ? 32 : kBN;
+    constexpr int NSUB = BN / 32;  // 32-key halves of a tile
     constexpr int BM = 32 * NW;
     constexpr int KS = D / 16;
     constexpr int DB = D / 32;
@@ -653,23 +656,25 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
 
         // S^T = K Q^T for the 64 keys of the tile (two 32-key halves); the K
         // reads run kLookTiled MFMAs ahead of their use.
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+        f32x16 s[NSUB];
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) s[sub] = f32x16{};
         {
-            constexpr int N = 2 * KS;
+            constexpr int N = NSUB * KS;
             u32x4 ring[kLookTiled];
             static_for<0, kLookTiled>([&](auto ic) __attribute__((always_inline)) {
                 constexpr int i = decltype(ic)::value;
-                ring[i] = tl.rm(kl, i & 1, i >> 1);
+                ring[i] = tl.rm(kl, i % NSUB, i / NSUB);
             });
             __builtin_amdgcn_sched_group_barrier(0x100, kLookTiled, 0);
             static_for<0, N>([&](auto ic) __attribute__((always_inline)) {
                 constexpr int i = decltype(ic)::value;
                 const u32x4 a = ring[i % kLookTiled];
                 if constexpr (i + kLookTiled < N) {
-                    ring[i % kLookTiled] = tl.rm(kl, (i + kLookTiled) & 1, (i + kLookTiled) >> 1);
+                    ring[i % kLookTiled] = tl.rm(kl, (i + kLookTiled) % NSUB, (i + kLookTiled) / NSUB);
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
-                s[i & 1] = mfma32<T>(a, qf[i >> 1], s[i & 1]);
+                s[i % NSUB] = mfma32<T>(a, qf[i / NSUB], s[i % NSUB]);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             });
         }
@@ -678,7 +683,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
             // The general kernel's score transform, with tanh from tanh_exp2.
             const bool cap = p.tanh_scale > 0.0f;
 #pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
+            for (int sub = 0; sub < NSUB; ++sub) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -696,7 +701,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
                                (wl >= 0 && kb < last_row + off - wl);
         if (need_mask) {
 #pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
+            for (int sub = 0; sub < NSUB; ++sub) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int col = kb + 32 * sub + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -706,7 +711,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
                 }
             }
         }
-        float mx = lane_max32(s[0], s[1]);
+        float mx = lane_max32(s[0], s[NSUB - 1]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m2 = mx * c;
         // Lazy rescale: the running max moves only when some row's max grows by
@@ -722,7 +727,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
         const float neg_m = (m == -INFINITY) ? 0.0f : -m;
         float rowsum = 0.0f;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
+        for (int sub = 0; sub < NSUB; ++sub) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float pv = fast_exp2(__builtin_fmaf(s[sub][r], c, neg_m));
@@ -735,15 +740,15 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
             // The row sum above is of the undropped probabilities; dropped ones
             // leave P (and O) only.
 #pragma unroll
-            for (int sub = 0; sub < 2; ++sub) {
+            for (int sub = 0; sub < NSUB; ++sub) {
                 apply_dropout_query_lane(drop, bh, static_cast<uint32_t>(row), static_cast<uint32_t>(kb / 32 + sub),
                                          hh, s[sub]);
             }
         }
         // P^T packed in place: k-slot j of group tt is key 16tt + 8(j/4) + 4hh + j%4.
-        u32x4 pk[4];
+        u32x4 pk[2 * NSUB];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
+        for (int tt = 0; tt < 2 * NSUB; ++tt) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 pk[tt][w] = pack2<T>(s[tt >> 1][8 * (tt & 1) + 2 * w], s[tt >> 1][8 * (tt & 1) + 2 * w + 1]);
@@ -751,7 +756,7 @@ __global__ void __launch_bounds__(256, D > 128 ? 1 : 2) flash_fwd_tiled_kernel(c
         }
         // O^T += V^T P^T (step i: db = i % DB, tt = i / DB), reads ahead as above.
         {
-            constexpr int N = 4 * DB;
+            constexpr int N = 2 * NSUB * DB;
             u32x4 ring[kLookTiled];
             static_for<0, kLookTiled>([&](auto ic) __attribute__((always_inline)) {
                 constexpr int i = decltype(ic)::value;
@@ -1406,12 +1411,13 @@ int64_t round128(int64_t n) { return (n + 127) / 128 * 128; }
 // 128 wide (the zero columns add nothing to Q K^T, and O's first D columns are
 // copied back): the general kernel runs them at a rounded-up width with
 // per-column masks (D = 48 236 -> 326, D = 112 341 -> 490 TFLOP/s padded).
-// Multiples of 32 keep their own size: the general kernel at D = 96 (579
-// TFLOP/s) beats the padded D = 128 tiles (444). Above 192 the D = 256 tiles
-// (~740 TFLOP/s at 256) beat the general kernel (~475 at D = 224) with the
-// padding's extra work and copies; at 192 and below they do not.
+// Multiples of 32 keep their own size below 128: the general kernel at D = 96
+// (579 TFLOP/s) beats the padded D = 128 tiles (444). Above 160 the D = 256
+// tiles (~975 TFLOP/s causal at 256) beat the general kernel (~500) with the
+// padding's extra work and copies (causal: D = 192 505 -> 547, D = 224 481 ->
+// 592); at 160 they do not (497 -> 451).
 int64_t fwd_work_dim(int64_t D) {
-    if (D > 192 && D < 256 && D % 8 == 0) return 256;
+    if (D > 160 && D < 256 && D % 8 == 0) return 256;
     if (D % 8 != 0 || D % 32 == 0 || D > 128) return D;
     return D < 64 ? 64 : 128;
 }
