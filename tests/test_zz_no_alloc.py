@@ -58,8 +58,10 @@ def test_noalloc_matches_workspace_entry(packed):
     lib = kcr_native.lib
     lib.kcr_flash_fwd_kvcache_noalloc_scratch_bytes.restype = ctypes.c_int64
     assert lib.kcr_flash_fwd_kvcache_noalloc_scratch_bytes() == 64 << 20
-    # second call smaller than the first, over the scratch the first left behind
+    # each call smaller than the one before, over the scratch it left behind
+    # (head size 256: four columns per lane in the split merge)
     for batch, rows, heads, kv_heads, cap, d, splits, seed in ((8, 4, 32, 8, 3000, 128, 16, 0),
+                                                              (4, 4, 16, 4, 2000, 256, 8, 2),
                                                               (3, 2, 8, 2, 700, 64, 5, 1)):
         q, kc, vc, cu, used, lse_shape = _case(batch, rows, heads, kv_heads, cap, d, packed, seed)
         tq = batch * rows
