@@ -417,7 +417,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Copies ROWS rows of a [rows, D] strided matrix (row stride `row_stride`
 // elements) into a swizzled tile by direct HBM -> LDS loads; rows at or past
 // `rows_valid` read as zero (buffer range check). The NW waves move 1 KB blocks
-// of 8 (D = 64) or 4 (D = 128) rows. NT: non-temporal copies (see dma_lds16).
+// of 8 (D = 64), 4 (D = 128) or 2 (D = 256) rows. NT: non-temporal copies (see
+// dma_lds16).
 template <int D, int NW, int ROWS, bool NT = false>
 __device__ __forceinline__ void copy_rows_dma(const uint16_t* base, int64_t row_stride, int rows_valid,
                                               uint16_t* tile, int wave, int lane) {

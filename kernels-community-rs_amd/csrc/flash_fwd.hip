@@ -1752,8 +1752,8 @@ void varlen_fwd_impl(const kcr_tensor* q, const kcr_tensor* k, const kcr_tensor*
             so_.copy_out();
             return;
         }
-        // Zero-padded copies for head sizes within 3/4 of 64 or 128 (see
-        // fwd_work_dim); the padded output starts as the caller's, so rows no
+        // Zero-padded copies for the head sizes fwd_work_dim widens to 64, 128
+        // or 256; the padded output starts as the caller's, so rows no
         // sequence covers come back unchanged.
         const int64_t DW = fwd_work_dim(D);
         const bool pad = DW != D;
