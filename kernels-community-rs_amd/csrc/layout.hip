@@ -3,10 +3,12 @@
 // 46-125, device/layout.rs:1-35), and the copy of an output written through a
 // packed buffer (host/forward/mod.rs:349-376).
 //
-// Design: one 64-lane wave per (batch, sequence, head) row; each lane moves
-// 2-byte elements with the row's own strides on both sides, so any source and
-// destination layout works (the staged side is always packed and aligned).
-// These copies only run for layouts the kernels cannot read directly.
+// Design: rows of (batch, sequence, head) copied with their own strides on
+// both sides. When both sides' bases, strides and widths are whole 16-byte
+// chunks (the zero-padded head-size copies, and staging of aligned layouts)
+// each lane moves 16-byte chunks, LPR lanes per row and 64 / LPR rows per
+// wave; otherwise one wave per row moves 2-byte elements, so any layout works
+// (the staged side is always packed and aligned).
 #include "attention.h"
 
 #include <algorithm>
@@ -38,6 +40,30 @@ __global__ void __launch_bounds__(64 * kCopyWaves) copy_rows_kernel(
     }
 }
 
+// The 16-byte chunk form: CD chunks copied, then zero chunks up to CZ. Row r
+// of rows < 2^31 is ((b * S) + s) * H + h.
+template <int LPR>
+__global__ void __launch_bounds__(64 * kCopyWaves) copy_rows_vec_kernel(
+    uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, uint32_t rows, uint32_t S, uint32_t H,
+    int CD, int CZ, int64_t sb, int64_t ss, int64_t sh, int64_t db, int64_t ds, int64_t dh) {
+    constexpr int RPW = 64 / LPR;  // rows per wave
+    const int lane = threadIdx.x & 63;
+    const int c0 = lane % LPR;
+    const uint32_t step = gridDim.x * kCopyWaves * RPW;
+    for (uint32_t r = (blockIdx.x * kCopyWaves + (threadIdx.x >> 6)) * RPW + lane / LPR; r < rows; r += step) {
+        const uint32_t h = r % H;
+        const uint32_t bs = r / H;
+        const uint32_t sq = bs % S;
+        const uint32_t b = bs / S;
+        const uint16_t* from = src + b * sb + sq * ss + h * sh;
+        uint16_t* to = dst + b * db + sq * ds + h * dh;
+        for (int c = c0; c < CZ; c += LPR) {
+            const u32x4 v = c < CD ? *reinterpret_cast<const u32x4*>(from + 8 * c) : u32x4{0, 0, 0, 0};
+            *reinterpret_cast<u32x4*>(to + 8 * c) = v;
+        }
+    }
+}
+
 // The tensor as [B, S, H, D] (packed 3-D tensors are [1, T, H, D]).
 struct Dims4 {
     int64_t shape[4];
@@ -60,6 +86,38 @@ void copy_rows(const kcr_tensor& dst, const kcr_tensor& src, hipStream_t s) {
     const Dims4 a = dims4(dst), b = dims4(src);
     const int64_t rows = a.shape[0] * a.shape[1] * a.shape[2];
     if (rows == 0 || a.shape[3] == 0) return;
+    const int64_t width = std::min(a.shape[3], b.shape[3]);
+    bool vec = width % 8 == 0 && a.shape[3] % 8 == 0 && rows < (int64_t{1} << 31) &&
+               reinterpret_cast<uintptr_t>(dst.data) % 16 == 0 && reinterpret_cast<uintptr_t>(src.data) % 16 == 0 &&
+               a.stride[3] == 1 && b.stride[3] == 1;
+    for (int i = 0; i < 3; ++i) {
+        vec = vec && (a.shape[i] == 1 || (a.stride[i] % 8 == 0 && b.stride[i] % 8 == 0));
+    }
+    if (vec) {
+        const int CZ = static_cast<int>(a.shape[3] / 8), CD = static_cast<int>(width / 8);
+        auto go = [&](auto lpr) {
+            constexpr int LPR = decltype(lpr)::value;
+            constexpr int RPB = kCopyWaves * (64 / LPR);  // rows per block
+            const int64_t blocks = std::min<int64_t>((rows + RPB - 1) / RPB, 65536);
+            copy_rows_vec_kernel<LPR><<<static_cast<unsigned>(blocks), 64 * kCopyWaves, 0, s>>>(
+                static_cast<uint16_t*>(dst.data), static_cast<const uint16_t*>(src.data),
+                static_cast<uint32_t>(rows), static_cast<uint32_t>(a.shape[1]), static_cast<uint32_t>(a.shape[2]),
+                CD, CZ, b.stride[0], b.stride[1], b.stride[2], a.stride[0], a.stride[1], a.stride[2]);
+        };
+        if (CZ <= 4) {
+            go(std::integral_constant<int, 4>{});
+        } else if (CZ <= 8) {
+            go(std::integral_constant<int, 8>{});
+        } else if (CZ <= 16) {
+            go(std::integral_constant<int, 16>{});
+        } else if (CZ <= 32) {
+            go(std::integral_constant<int, 32>{});
+        } else {
+            go(std::integral_constant<int, 64>{});
+        }
+        check_launch("launch copy_rows");
+        return;
+    }
     const int64_t blocks = std::min<int64_t>((rows + kCopyWaves - 1) / kCopyWaves, 65536);
     copy_rows_kernel<<<static_cast<unsigned>(blocks), 64 * kCopyWaves, 0, s>>>(
         static_cast<uint16_t*>(dst.data), static_cast<const uint16_t*>(src.data), rows, a.shape[1],
