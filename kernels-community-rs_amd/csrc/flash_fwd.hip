@@ -1412,12 +1412,12 @@ int64_t round128(int64_t n) { return (n + 127) / 128 * 128; }
 // copied back): the general kernel runs them at a rounded-up width with
 // per-column masks (D = 48 236 -> 326, D = 112 341 -> 490 TFLOP/s padded).
 // Multiples of 32 keep their own size below 128: the general kernel at D = 96
-// (579 TFLOP/s) beats the padded D = 128 tiles (444). Above 160 the D = 256
-// tiles (~975 TFLOP/s causal at 256) beat the general kernel (~500) with the
-// padding's extra work and copies (causal: D = 192 505 -> 547, D = 224 481 ->
-// 592); at 160 they do not (497 -> 451).
+// (579 TFLOP/s) beats the padded D = 128 tiles (444). Above 128 the D = 256
+// tiles (~975 TFLOP/s causal at 256) beat the general kernel with the
+// padding's extra work and copies (causal: D = 136 250 -> 455, D = 160 503 ->
+// 541, D = 192 535 -> 634).
 int64_t fwd_work_dim(int64_t D) {
-    if (D > 160 && D < 256 && D % 8 == 0) return 256;
+    if (D > 128 && D < 256 && D % 8 == 0) return 256;
     if (D % 8 != 0 || D % 32 == 0 || D > 128) return D;
     return D < 64 ? 64 : 128;
 }
