@@ -248,7 +248,7 @@ def _wl_fa_varlen(kind):
     return make
 
 
-def wl_fa_kvcache_decode():
+def wl_fa_kvcache_decode(graph=False):
     """flash_attn_with_kvcache decode step (an inference path with no benchmark
     config of its own): B=16 sequences with 8191 cached tokens each, one new
     token appended, Hq=32, Hkv=8, D=128 bf16, causal, automatic key splits.
@@ -269,9 +269,21 @@ def wl_fa_kvcache_decode():
         flash_attn2_rs.flash_attn_with_kvcache(q, kc, vc, kn, vn, cache_seqlens=lengths, causal=True,
                                                num_splits=0)
 
+    if graph:
+        # The same step captured once and replayed: no Python or launch cost
+        # per step (the append position is fixed, as in the eager run).
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run()
+        torch.cuda.current_stream().wait_stream(side)
+        captured = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(captured):
+            run()
+        run = captured.replay
     return dict(run=run, work=2 * b * cap * hkv * d * 2, bound="hbm", kernel="flash_fwd_tiled",
                 config={"B": b, "Hq": hq, "Hkv": hkv, "D": d, "cache_len": cap, "new_tokens": 1,
-                        "causal": True, "dtype": "bf16"}, cpu=None)
+                        "causal": True, "dtype": "bf16", **({"cuda_graph": True} if graph else {})}, cpu=None)
 
 
 def wl_hbm_copy():
@@ -404,6 +416,7 @@ WORKLOADS = {
     "gelu_tanh_and_mul": _wl_gated("gelu_tanh_and_mul"),
     "silu": wl_silu,
     "fa_kvcache_decode": wl_fa_kvcache_decode,
+    "fa_kvcache_decode_graph": lambda: wl_fa_kvcache_decode(graph=True),
     "fa_fwd_split": wl_fa_split,
     "fa_fwd_config1": wl_fa_config1,
     "hbm_stream_1to1": _wl_hbm_stream(1),
@@ -413,7 +426,7 @@ WORKLOADS = {
 }
 OPT_IN = ("hbm_copy", "gemm_ceiling", "fa_fwd_causal_alibi", "fa_fwd_causal_softcap", "fa_bwd_causal_alibi",
           "fa_bwd_causal_softcap", "fa_fwd_causal_d112", "fa_bwd_causal_d96",
-          "fa_fwd_causal_d256", "fa_bwd_causal_d256")
+          "fa_fwd_causal_d256", "fa_bwd_causal_d256", "fa_kvcache_decode_graph")
 DEFAULT_ORDER = [n for n in WORKLOADS if n not in OPT_IN]
 # Ops whose CPU baseline is timed in every default run (bounded samples).
 CPU_OPS = ("fa_fwd_causal", "fa_fwd_config1", "rms_norm", "silu_and_mul")
