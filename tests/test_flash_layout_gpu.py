@@ -129,3 +129,28 @@ def test_varlen_and_backward_misaligned_match_contiguous():
                     None, True, -1, -1, 0.0, 0.0, None)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+def test_padded_head_size_from_strided_views():
+    """Head size 72 (run through zero-padded 128-wide copies) with q and dout
+    as transposed [B, H, S, D] views and k, v with a size-1 batch dimension of
+    odd stride: the padded copies read the views in 16-byte chunks; forward and
+    backward give the same bits as contiguous inputs."""
+    import flash_attn2_rs
+
+    B, S, H, Hk, D = 1, 150, 4, 2, 72
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, H, S, D, generator=g).bfloat16().cuda().transpose(1, 2)
+    dout = torch.randn(B, H, S, D, generator=g).bfloat16().cuda().transpose(1, 2)
+    kv = torch.randn(2, S, Hk, D, generator=g).bfloat16().cuda()
+    k = kv[0].as_strided((1, S, Hk, D), (7, Hk * D, D, 1))
+    v = kv[1].as_strided((1, S, Hk, D), (13, Hk * D, D, 1))
+    assert not q.is_contiguous() and k.stride(0) % 8 != 0
+    o1, l1, _, _ = flash_attn2_rs.fwd(q, k, v, is_causal=True)
+    o2, l2, _, _ = flash_attn2_rs.fwd(q.contiguous(), k.contiguous(), v.contiguous(), is_causal=True)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    g1 = flash_attn2_rs.bwd(dout, q, k, v, o1, l1, is_causal=True)
+    g2 = flash_attn2_rs.bwd(dout.contiguous(), q.contiguous(), k.contiguous(), v.contiguous(), o2, l2,
+                            is_causal=True)
+    for a, b in zip(g1[:3], g2[:3]):
+        assert torch.equal(a, b)
